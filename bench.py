@@ -1,0 +1,260 @@
+#!/usr/bin/env python3
+"""Benchmark of the INT4 superblock dequant-GEMM on one MI355X.
+
+Workload (default): the FFN gate/up projection K=2048 x M=5504, weights
+~N(0, 0.02) (seed 1002) quantized to 144-byte superblocks (2048*5504/256 =
+44,032 records, 6.34 MB), fp16 activations ~N(0, 1), swept over N = 1, 2, 4,
+8, 16, 32 parallel traces.  One "step" is one sweep: six projections, one per
+N, each on a different copy of the weight stream (copies rotate so that the
+256 MB Infinity Cache cannot serve repeats: >= 300 MB of distinct records).
+
+Printed: one JSON line with the whole-job throughput (tokens/s over the
+sweep), per-N microseconds/call, HBM GB/s and roofline fraction, the
+roofline of the dominant kernel and the CPU baseline (the numpy oracle on the
+host cores, a bounded sample).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, 8 TB/s
+CONFIGS = {
+    # name: (K, M, weight std, weight seed, outlier fraction, default Ns)
+    "cfg1": (2048, 2048, 0.02, 1001, 0.0, [8]),
+    "cfg2": (2048, 5504, 0.02, 1002, 0.0, [1, 2, 4, 8, 16, 32]),
+    "cfg3": (3072, 8192, 0.02, 1003, 0.0, [1, 2, 4, 8, 16, 32]),
+    "cfg5": (8192, 28672, 0.01, 1005, 0.001, [1, 32]),
+}
+WORKLOAD_NAMES = {
+    "cfg1": "int4 superblock projection 2048x2048",
+    "cfg2": "int4 superblock FFN gate/up projection K=2048 M=5504, N sweep 1..32",
+    "cfg3": "int4 superblock FFN projection K=3072 M=8192, N sweep 1..32",
+    "cfg5": "int4 superblock projection K=8192 M=28672 (70B-class FFN, 0.1% 8-sigma outliers)",
+}
+ROTATE_BYTES = 300 * 1024 * 1024
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def algo_bytes(N: int, K: int, M: int) -> int:
+    """Algorithmic HBM bytes of one call: records (0.5625 B/weight) + fp16 X + fp32 Y."""
+    return 144 * K * M // 256 + 2 * N * K + 4 * N * M
+
+
+def cpu_baseline(K, M, ns, blob, budget_s: float):
+    """The oracle on the host: decode the records, then a float32 matmul (the
+    reference CPU path), timed per N on a bounded number of repetitions."""
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from oracle import superblock_oracle as O
+
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max((p.get("num_threads") or 1) for p in threadpool_info()) if threadpool_info() else 1
+    except Exception:  # threadpoolctl missing
+        threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    per_n = {}
+    per_n_budget = budget_s / len(ns)
+    total_t, total_tok = 0.0, 0
+    for N in ns:
+        x = O.synthetic_activations(N, K, 2200 + N)
+        O.gemm_ref(x, blob, K, M)  # warm
+        times = []
+        t_start = time.perf_counter()
+        while len(times) < 3 or (time.perf_counter() - t_start < per_n_budget and len(times) < 10):
+            t0 = time.perf_counter()
+            O.gemm_ref(x, blob, K, M)
+            times.append(time.perf_counter() - t0)
+        med = float(np.median(times))
+        per_n[N] = {"ms_per_call": med * 1e3, "tok_s": N / med, "reps": len(times)}
+        total_t += med
+        total_tok += N
+    return {
+        "value": total_tok / total_t,
+        "unit": "tok/s",
+        "cores": int(threads),
+        "kind": "port",
+        "sample": (f"numpy oracle: decode {K}x{M} records then float32 matmul, per N in {ns}, "
+                   f"median of 3-10 reps each (~{budget_s:.0f} s budget); host os.cpu_count()={os.cpu_count()}, "
+                   f"affinity={len(os.sched_getaffinity(0))}"),
+        "per_n": per_n,
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="cfg2", choices=sorted(CONFIGS))
+    ap.add_argument("--ns", default=None, help="comma-separated N values (default: the config's)")
+    ap.add_argument("--algo", type=int, default=0, help="0 auto, 1 dot2, 2 mfma")
+    ap.add_argument("--splits", type=int, default=0)
+    ap.add_argument("--calls", type=int, default=200, help="timed launches per N for the per-N table")
+    ap.add_argument("--cpu-budget", type=float, default=15.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--graph", action="store_true", help="replay the sweep from a HIP graph")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})",
+              file=sys.stderr)
+        return 2
+
+    import torch
+    from moat_amd import _lib
+    from moat_amd.dequant import _gemm_into, quantize_to_superblocks
+
+    lib = _lib.load()
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    K, M, std, seed, outl, default_ns = CONFIGS[args.config]
+    ns = [int(v) for v in args.ns.split(",")] if args.ns else default_ns
+
+    rng = np.random.default_rng(seed)
+    log(f"[bench] building {args.config}: K={K} M={M}")
+    w = rng.standard_normal((K, M), dtype=np.float32) * np.float32(std)
+    if outl:
+        n_out = int(round(outl * K * M))
+        pos = rng.choice(K * M, size=n_out, replace=False)
+        w.reshape(-1)[pos] = rng.choice(np.array([-1.0, 1.0], np.float32), size=n_out) * np.float32(8 * std)
+    blob0 = quantize_to_superblocks(torch.from_numpy(w).to(dev))  # (S, 144) uint8 on the GPU
+    del w
+    sb_bytes = blob0.numel()
+    copies = max(2, -(-ROTATE_BYTES // sb_bytes))
+    blobs = [blob0] + [blob0.clone() for _ in range(copies - 1)]
+    log(f"[bench] {copies} copies of {sb_bytes / 1e6:.2f} MB records ({copies * sb_bytes / 1e6:.0f} MB rotated)")
+
+    xs = {N: torch.from_numpy(np.random.default_rng(2000 + 100 * 2 + N).standard_normal((N, K), dtype=np.float32)
+                              .astype(np.float16)).to(dev) for N in ns}
+    ys = {N: torch.empty((N, M), dtype=torch.float32, device=dev) for N in ns}
+    stream = torch.cuda.current_stream()
+
+    def one_call(N, i):
+        _gemm_into(xs[N], blobs[i % copies], ys[N], K, M, args.algo, args.splits)
+
+    counter = [0]
+
+    def sweep():
+        for N in ns:
+            one_call(N, counter[0])
+            counter[0] += 1
+
+    # per-N table: back-to-back launches between HIP events on the launch stream
+    per_n = {}
+    for N in ns:
+        for i in range(10):
+            one_call(N, i)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for i in range(args.calls):
+            one_call(N, i)
+        e1.record(stream)
+        e1.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / args.calls
+        b = algo_bytes(N, K, M)
+        per_n[N] = {"us_per_call": round(us, 3), "gbs": round(b / us / 1e3, 1),
+                    "roofline_frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4), "tok_s": round(N / us * 1e6, 1),
+                    "algo_bytes": b}
+        log(f"[bench] N={N:2d}: {us:8.2f} us/call  {b / us / 1e3:7.0f} GB/s  "
+            f"{100 * b / us / 1e3 / HBM_PEAK_GBS:5.1f}% of 8 TB/s")
+    t1 = per_n[ns[0]]["us_per_call"] / ns[0]
+    for N in ns:
+        per_n[N]["per_token_speedup_vs_first"] = round(t1 / (per_n[N]["us_per_call"] / N), 3)
+
+    graph = None
+    if args.graph:
+        # capture on a stream whose workspace already exists (no allocation or
+        # clearing inside the graph)
+        cap = torch.cuda.Stream()
+        cap.wait_stream(stream)
+        with torch.cuda.stream(cap):
+            for _ in range(3):
+                sweep()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=cap):
+            for i, N in enumerate(ns):
+                one_call(N, i)
+        torch.cuda.synchronize()
+
+    def step():
+        if graph is not None:
+            graph.replay()
+        else:
+            sweep()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(args.steps):
+        step()
+    e1.record(stream)
+    e1.synchronize()
+    torch.cuda.synchronize()
+    ms_step = e0.elapsed_time(e1) / args.steps
+    tokens = sum(ns)
+    value = tokens / (ms_step / 1e3)
+    log(f"[bench] sweep: {ms_step * 1e3:.1f} us/step, {value:.0f} tok/s")
+
+    dom = max(ns, key=lambda n: per_n[n]["us_per_call"])
+    roof = {
+        "bound": "hbm",
+        "achieved": per_n[dom]["gbs"],
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": per_n[dom]["roofline_frac"],
+        "traffic": None,
+        "kernel": f"int4 gemm N={dom} ({per_n[dom]['us_per_call']} us/launch, {per_n[dom]['algo_bytes']} algorithmic B)",
+    }
+    traffic_file = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                                f"traffic_{args.config}.json")
+    if os.path.exists(traffic_file):
+        with open(traffic_file) as f:
+            tr = json.load(f).get(str(dom))
+        if tr is not None:
+            roof["traffic"] = tr
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("[bench] CPU baseline (numpy oracle) ...")
+        cpu = cpu_baseline(K, M, ns, blob0.cpu().numpy(), args.cpu_budget)
+        log(f"[bench] CPU baseline: {cpu['value']:.1f} tok/s on {cpu['cores']} threads")
+
+    out = {
+        "metric": "INT4 dequant-GEMM µs/call, HBM GB/s (% roofline), tok/s at N=1..32",
+        "value": round(value, 1),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int4-superblock weights, fp16 activations, fp32 accumulate",
+        "data": "synthetic",
+        "config": {"workload": WORKLOAD_NAMES[args.config], "K": K, "M": M, "ns": ns,
+                   "weight_copies_rotated": copies, "graph": bool(args.graph), "algo": args.algo,
+                   "splits": args.splits},
+        "per_n": {str(k): v for k, v in per_n.items()},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

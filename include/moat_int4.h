@@ -1,0 +1,178 @@
+/*
+ * moat_int4.h -- C ABI of libmoat_int4.so, the MI355X (gfx950) implementation
+ * of moat's INT4 superblock path.
+ *
+ * Data format: a weight matrix W[K][M] (row-major, flat index k*M + m) is a
+ * stream of 144-byte superblocks, one per 256 consecutive flat elements:
+ * bytes [0,16) hold 8 little-endian fp16 scales (group g = elements 32g..32g+31),
+ * bytes [16,144) hold nibble pairs, element 2j in the LOW nibble of byte j and
+ * element 2j+1 in the HIGH nibble, each stored as q+8 in [0,15]
+ * (antigravity-engine/src/shaders/batched_gemm.metal:16-20, 146-154;
+ * src/dequant.py:116-147).  A dequantized element is fp16(f32(q) * f32(scale)).
+ *
+ * Conventions (after antigravity-engine/src/antigravity_c_api.h:15-17, 129, 161):
+ *  - extern "C", plain pointers and sizes; every pointer is a DEVICE pointer
+ *    owned by the caller (no allocation inside any entry point);
+ *  - int32 status: 0 = ok, negative = error (see MOAT_ERR_*); arguments are
+ *    validated BEFORE any HIP call, so a bad call has no side effect;
+ *  - work is enqueued on `stream` and returns without synchronising;
+ *  - no mutable globals: calls on distinct streams with distinct output and
+ *    workspace buffers may run concurrently.
+ *
+ * The reference has no C ABI for this path (its hot path is the numpy module
+ * src/dequant.py and the Metal kernels in batched_gemm.metal); each entry
+ * point names the reference function or kernel whose result it reproduces.
+ */
+#ifndef MOAT_INT4_H
+#define MOAT_INT4_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MOAT_INT4_VERSION_MAJOR 0
+#define MOAT_INT4_VERSION_MINOR 1
+
+/* status codes */
+#define MOAT_OK 0
+#define MOAT_ERR_INVALID (-2)     /* bad shape, size, pointer or alignment */
+#define MOAT_ERR_HIP (-3)         /* a HIP runtime call or kernel launch failed */
+#define MOAT_ERR_WORKSPACE (-4)   /* workspace missing or too small */
+
+/* element types for the typed entry points */
+#define MOAT_DTYPE_F32 0
+#define MOAT_DTYPE_F16 1
+#define MOAT_DTYPE_I8 2
+#define MOAT_DTYPE_F64 3
+#define MOAT_DTYPE_I64 4
+
+/* quantizer scale rules */
+#define MOAT_SCALE_F32 0 /* divide by the float32 scale: src/dequant.py:47-53 */
+#define MOAT_SCALE_F16 1 /* divide by the fp16-rounded scale: antigravity-engine/src/dequant.py:56-58 */
+
+/* GEMM kernel choice */
+#define MOAT_GEMM_AUTO 0
+#define MOAT_GEMM_DOT2 1 /* VALU: v_dot2_f32_f16 with a wavefront reduction */
+#define MOAT_GEMM_MFMA 2 /* matrix cores: v_mfma_f32_16x16x32_f16 */
+
+/* MAJOR*100 + MINOR */
+int32_t moat_int4_version(void);
+
+/* Static text for a status code. */
+const char* moat_int4_status_string(int32_t status);
+
+/*
+ * Decode n_superblocks 144-byte records into fp16 (n_superblocks*256 values,
+ * flat order).  Bit-exact with src/dequant.py:116-147
+ * (unpack_superblock_weights) and antigravity-engine/src/shaders/batched_gemm.metal:41-66
+ * (dequantize_superblocks_kernel).  superblocks and out: 16-byte aligned.
+ */
+int32_t moat_int4_dequant(const uint8_t* superblocks, int64_t n_superblocks,
+                          uint16_t* out_f16, hipStream_t stream);
+
+/*
+ * Y[n][M] (fp32) = X[n][K] (fp16) @ deq(W)[K][M], the batched decode
+ * projection for n = 1..32 parallel traces.  Semantics: the reference CPU
+ * path, dequantize (src/dequant.py:116-147) then float32 matmul
+ * (antigravity-engine/tests/test_batched_speed.py:39-42); replaces the fused
+ * kernel antigravity-engine/src/shaders/batched_gemm.metal:116-169.
+ * Preconditions: 1 <= n <= 32, k >= 1, m >= 32, m % 32 == 0, (k*m) % 256 == 0;
+ * x 2-byte aligned, superblocks 16-byte aligned, y 4-byte aligned.
+ * workspace: device memory of moat_int4_gemm_workspace_size() bytes (may be
+ * NULL when that size is 0), zero-filled once before first use (e.g. with
+ * moat_int4_workspace_clear); every call leaves its counter words at zero
+ * again.  Calls that share a workspace must not overlap.
+ */
+int64_t moat_int4_gemm_workspace_size(int32_t n, int32_t k, int32_t m);
+int32_t moat_int4_gemm(const uint16_t* x_f16, const uint8_t* superblocks, float* y_f32,
+                       int32_t n, int32_t k, int32_t m,
+                       void* workspace, int64_t workspace_bytes, hipStream_t stream);
+
+/* Same product with the kernel (MOAT_GEMM_*) and the number of K slices
+ * (splits >= 1; 0 = automatic) chosen by the caller: for measurement and for
+ * testing each kernel at every n.  Workspace size from the _ex query. */
+int64_t moat_int4_gemm_ex_workspace_size(int32_t n, int32_t k, int32_t m, int32_t algo, int32_t splits);
+int32_t moat_int4_gemm_ex(const uint16_t* x_f16, const uint8_t* superblocks, float* y_f32,
+                          int32_t n, int32_t k, int32_t m, int32_t algo, int32_t splits,
+                          void* workspace, int64_t workspace_bytes, hipStream_t stream);
+
+/* Zero `bytes` bytes of device memory with a kernel (no memset node). */
+int32_t moat_int4_workspace_clear(void* workspace, int64_t bytes, hipStream_t stream);
+
+/*
+ * Group quantizer: for each group of group_size values (w_dtype F32, F16 or F64;
+ * F64 is rounded to float32 first, as astype(np.float32) does),
+ * alpha = max|w|, s = (alpha == 0 ? 1 : alpha / 7) in float32; q =
+ * clip(rint_half_even(w / d), -8, 7) with d = s (MOAT_SCALE_F32, surface A:
+ * src/dequant.py:26-55) or d = fp16(s) (MOAT_SCALE_F16, surface B:
+ * antigravity-engine/src/dequant.py:22-60); scales_out = fp16(s).
+ * n % group_size == 0.  A NaN quotient gives q = 0.
+ */
+int32_t moat_int4_quantize(const void* w, int32_t w_dtype, int64_t n, int32_t group_size,
+                           int32_t scale_mode, int8_t* q_out, uint16_t* scales_out,
+                           hipStream_t stream);
+
+/*
+ * Serialize q (int8, values taken mod 16 after +8) and fp16 scales into
+ * n_superblocks 144-byte records (the writer for the format above; the
+ * inverse of src/dequant.py:116-147; nibble rule of
+ * antigravity-engine/src/dequant.py:119-124).  superblocks_out 16-byte aligned.
+ */
+int32_t moat_int4_pack_superblocks(const int8_t* q, const uint16_t* scales_f16,
+                                   int64_t n_superblocks, uint8_t* superblocks_out,
+                                   hipStream_t stream);
+
+/* Quantize (group 32, rule scale_mode) and serialize in one pass: n % 256 == 0. */
+int32_t moat_int4_quantize_pack(const void* w, int32_t w_dtype, int64_t n, int32_t scale_mode,
+                                uint8_t* superblocks_out, hipStream_t stream);
+
+/* Nibble pairs without headers, antigravity-engine/src/dequant.py:119-124
+ * (repack_to_superblocks' payload); n even. */
+int32_t moat_int4_pack_nibbles(const int8_t* q, int64_t n, uint8_t* packed_out, hipStream_t stream);
+
+/* Inverse, antigravity-engine/src/dequant.py:135-156 (unpack_superblock):
+ * 2*n_bytes int8 values in [-8, 7]. */
+int32_t moat_int4_unpack_nibbles(const uint8_t* packed, int64_t n_bytes, int8_t* q_out,
+                                 hipStream_t stream);
+
+/*
+ * Per-group dequant of unpacked values, fp16(f32(q) * f32(scales[g])) for the
+ * first n_groups*group_size elements (the caller zero-fills any tail).
+ * q_dtype: I8, I64 or F32; scale_dtype: F16, F32 or F64 (one per group; an
+ * F64 scale is rounded to float32 first, like numpy's float32 * float).
+ * table_mode 0: arithmetic_dequantize (antigravity-engine/src/dequant.py:223-252).
+ * table_mode 1: lut_dequantize (:183-220), a 16-entry table indexed by q+8
+ * with Python's negative-index wrap (q given as I8 or as I64 already reduced
+ * to int16); an index outside [-16, 16) leaves the element 0 and sets
+ * *err_flag to 1 (err_flag may be NULL in mode 0).
+ */
+int32_t moat_int4_group_dequant(const void* q, int32_t q_dtype, const void* scales, int32_t scale_dtype,
+                                int64_t n_groups, int32_t group_size, int32_t table_mode,
+                                uint16_t* out_f16, int32_t* err_flag, hipStream_t stream);
+
+/*
+ * Clipped table gather of src/dequant.py:79-112 (lut_dequantize_fp16):
+ * out[i] = lut[row(i)][clip(idx(q[i]), 0, lut_len-1)], row(i) = i / (n / lut_rows).
+ * index_mode 0: idx = q + 8; 1: idx = int32(q) + 8 (32-bit wrap); 2: idx = int32(q).
+ * q is int64, lut fp16 [lut_rows][lut_len]; n % lut_rows == 0.
+ */
+int32_t moat_int4_lut_gather(const int64_t* q, int64_t n, int32_t index_mode,
+                             const uint16_t* lut_f16, int64_t lut_rows, int32_t lut_len,
+                             uint16_t* out_f16, hipStream_t stream);
+
+/* *flag_out = 1 if any q[i] < 0 else 0 (int32 on the device); the branch test
+ * of src/dequant.py:90. */
+int32_t moat_int4_any_negative(const int64_t* q, int64_t n, int32_t* flag_out, hipStream_t stream);
+
+/* Round F32 or F64 values to fp16, nearest-even, one rounding (numpy's astype(float16)). */
+int32_t moat_int4_to_f16(const void* src, int32_t src_dtype, int64_t n, uint16_t* out_f16,
+                         hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MOAT_INT4_H */

@@ -1,0 +1,82 @@
+"""ctypes binding of libmoat_int4.so (the gfx950 kernels).
+
+Follows the reference's FFI pattern (``antigravity-engine/src/native_bridge.py:95-160``:
+explicit argtypes/restypes; a nonzero status becomes a Python exception),
+with device pointers from torch tensors and torch's current HIP stream.
+
+There is no fallback: a missing library or a missing GPU raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libmoat_int4.so")
+
+MOAT_OK = 0
+MOAT_ERR_INVALID = -2
+MOAT_ERR_HIP = -3
+MOAT_ERR_WORKSPACE = -4
+
+DTYPE_F32, DTYPE_F16, DTYPE_I8, DTYPE_F64, DTYPE_I64 = 0, 1, 2, 3, 4
+SCALE_F32, SCALE_F16 = 0, 1
+GEMM_AUTO, GEMM_DOT2, GEMM_MFMA = 0, 1, 2
+
+_P = ctypes.c_void_p
+_I32 = ctypes.c_int32
+_I64 = ctypes.c_int64
+
+# name -> (restype, argtypes); every symbol declared in include/moat_int4.h
+SIGNATURES = {
+    "moat_int4_version": (_I32, []),
+    "moat_int4_status_string": (ctypes.c_char_p, [_I32]),
+    "moat_int4_dequant": (_I32, [_P, _I64, _P, _P]),
+    "moat_int4_gemm_workspace_size": (_I64, [_I32, _I32, _I32]),
+    "moat_int4_gemm": (_I32, [_P, _P, _P, _I32, _I32, _I32, _P, _I64, _P]),
+    "moat_int4_gemm_ex_workspace_size": (_I64, [_I32, _I32, _I32, _I32, _I32]),
+    "moat_int4_gemm_ex": (_I32, [_P, _P, _P, _I32, _I32, _I32, _I32, _I32, _P, _I64, _P]),
+    "moat_int4_workspace_clear": (_I32, [_P, _I64, _P]),
+    "moat_int4_quantize": (_I32, [_P, _I32, _I64, _I32, _I32, _P, _P, _P]),
+    "moat_int4_pack_superblocks": (_I32, [_P, _P, _I64, _P, _P]),
+    "moat_int4_quantize_pack": (_I32, [_P, _I32, _I64, _I32, _P, _P]),
+    "moat_int4_pack_nibbles": (_I32, [_P, _I64, _P, _P]),
+    "moat_int4_unpack_nibbles": (_I32, [_P, _I64, _P, _P]),
+    "moat_int4_group_dequant": (_I32, [_P, _I32, _P, _I32, _I64, _I32, _I32, _P, _P, _P]),
+    "moat_int4_lut_gather": (_I32, [_P, _I64, _I32, _P, _I64, _I32, _P, _P]),
+    "moat_int4_any_negative": (_I32, [_P, _I64, _P, _P]),
+    "moat_int4_to_f16": (_I32, [_P, _I32, _I64, _P, _P]),
+}
+
+_lib = None
+
+
+def load(path: str = LIB_PATH) -> ctypes.CDLL:
+    """Load the library once.  torch is imported first so that the library
+    binds to the same HIP runtime as torch's tensors and streams."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    import torch  # noqa: F401  (loads torch's libamdhip64 before ours)
+
+    if not os.path.exists(path):
+        raise RuntimeError(
+            f"{path} is missing: build it with `python -m moat_amd.build_lib` "
+            "(moat_amd has no CPU fallback)")
+    lib = ctypes.CDLL(path)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def check(status: int, what: str) -> None:
+    if status == MOAT_OK:
+        return
+    msg = load().moat_int4_status_string(status).decode()
+    if status in (MOAT_ERR_INVALID, MOAT_ERR_WORKSPACE):
+        raise ValueError(f"{what}: {msg} (status {status})")
+    raise RuntimeError(f"{what}: {msg} (status {status})")

@@ -1,0 +1,241 @@
+// C ABI of libmoat_int4.so: argument validation (before any HIP call),
+// planning of the GEMM launch, and dispatch to the kernels.
+#include <stdint.h>
+
+#include <hip/hip_runtime.h>
+
+#include "../../include/moat_int4.h"
+
+namespace moat {
+hipError_t launch_dequant_stream(const uint8_t* sb, int64_t n_sb, uint16_t* out, hipStream_t st);
+hipError_t launch_pack_nibbles(const int8_t* q, int64_t n, uint8_t* packed, hipStream_t st);
+hipError_t launch_unpack_nibbles(const uint8_t* packed, int64_t n_bytes, int8_t* q, hipStream_t st);
+hipError_t launch_group_dequant(const void* q, int q_dtype, const void* scales, int scale_dtype, int64_t n_groups,
+                                int group_size, int table_mode, uint16_t* out, int32_t* err_flag, hipStream_t st);
+hipError_t launch_lut_gather(const int64_t* q, int64_t n, int index_mode, const uint16_t* lut, int64_t lut_rows,
+                             int lut_len, uint16_t* out, hipStream_t st);
+hipError_t launch_any_negative(const int64_t* q, int64_t n, int32_t* flag, hipStream_t st);
+hipError_t launch_to_f16(const void* src, int src_dtype, int64_t n, uint16_t* out, hipStream_t st);
+hipError_t launch_clear(void* p, int64_t bytes, hipStream_t st);
+hipError_t launch_quantize(const void* w, int dtype, int64_t n, int gsize, int scale_mode, int8_t* q,
+                           uint16_t* scales, hipStream_t st);
+hipError_t launch_pack_superblocks(const int8_t* q, const uint16_t* scales, int64_t n_sb, uint8_t* sb,
+                                   hipStream_t st);
+hipError_t launch_quantize_pack(const void* w, int dtype, int64_t n, int scale_mode, uint8_t* sb, hipStream_t st);
+int gemm_col_tiles(int m);
+int gemm_rounds(int k);
+hipError_t launch_gemm(int algo, const uint16_t* x, const uint8_t* sb, float* y, int n, int k, int m, int splits,
+                       float* partials, uint32_t* counters, hipStream_t stream);
+}  // namespace moat
+
+namespace {
+
+constexpr int kMaxN = 32;
+constexpr int kMaxDot2N = 8;
+constexpr int64_t kCounterAlign = 256;
+
+bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+int32_t status_of(hipError_t e) { return e == hipSuccess ? MOAT_OK : MOAT_ERR_HIP; }
+
+struct GemmPlan {
+  int algo;
+  int splits;
+  int64_t counter_bytes;
+  int64_t workspace_bytes;
+};
+
+bool gemm_shape_ok(int32_t n, int32_t k, int32_t m) {
+  if (n < 1 || n > kMaxN || k < 1 || m < 32 || (m % 32) != 0) return false;
+  if (((int64_t)k * (int64_t)m) % 256 != 0) return false;
+  // byte offsets of one 32-row round are 32-bit in the kernels
+  if ((int64_t)m * 33 * 18 > (int64_t)0xFFFFFFFF) return false;
+  return true;
+}
+
+// Kernel and K-split choice.  The split count trades parallelism (a column
+// tile is 128 columns, so M/128 workgroups alone leave most of the 256 CUs
+// idle at these sizes) against partial-sum traffic, which is
+// splits * N * M * 8 bytes against 0.5625 * K * M bytes of weights; it is kept
+// below a quarter of the weight stream.
+GemmPlan plan_gemm(int32_t n, int32_t k, int32_t m, int32_t algo, int32_t splits) {
+  GemmPlan p;
+  if (algo == MOAT_GEMM_AUTO) algo = (n <= 2) ? MOAT_GEMM_DOT2 : MOAT_GEMM_MFMA;
+  p.algo = algo;
+  const int tiles = moat::gemm_col_tiles(m);
+  const int rounds = moat::gemm_rounds(k);
+  if (splits <= 0) {
+    const int target_wgs = 640;
+    int s = (target_wgs + tiles / 2) / tiles;
+    const int by_rounds = rounds / 4 > 0 ? rounds / 4 : 1;
+    const double cap_d = 0.25 * 0.5625 * (double)k / (8.0 * (double)n);
+    const int by_traffic = cap_d >= 1.0 ? (int)cap_d : 1;
+    if (s > by_rounds) s = by_rounds;
+    if (s > by_traffic) s = by_traffic;
+    if (s < 1) s = 1;
+    splits = s;
+  }
+  if (splits > rounds) splits = rounds;
+  p.splits = splits;
+  if (splits > 1) {
+    p.counter_bytes = ((int64_t)tiles * 4 + kCounterAlign - 1) / kCounterAlign * kCounterAlign;
+    p.workspace_bytes = p.counter_bytes + (int64_t)splits * n * m * 4;
+  } else {
+    p.counter_bytes = 0;
+    p.workspace_bytes = 0;
+  }
+  return p;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t moat_int4_version(void) { return MOAT_INT4_VERSION_MAJOR * 100 + MOAT_INT4_VERSION_MINOR; }
+
+const char* moat_int4_status_string(int32_t status) {
+  switch (status) {
+    case MOAT_OK: return "ok";
+    case MOAT_ERR_INVALID: return "invalid argument (shape, size, pointer or alignment)";
+    case MOAT_ERR_HIP: return "HIP runtime error";
+    case MOAT_ERR_WORKSPACE: return "workspace missing or too small";
+    default: return "unknown status";
+  }
+}
+
+int32_t moat_int4_dequant(const uint8_t* superblocks, int64_t n_superblocks, uint16_t* out_f16, hipStream_t stream) {
+  if (n_superblocks < 0) return MOAT_ERR_INVALID;
+  if (n_superblocks == 0) return MOAT_OK;
+  if (!superblocks || !out_f16 || !aligned(superblocks, 16) || !aligned(out_f16, 16)) return MOAT_ERR_INVALID;
+  return status_of(moat::launch_dequant_stream(superblocks, n_superblocks, out_f16, stream));
+}
+
+int64_t moat_int4_gemm_ex_workspace_size(int32_t n, int32_t k, int32_t m, int32_t algo, int32_t splits) {
+  if (!gemm_shape_ok(n, k, m) || algo < 0 || algo > 2 || splits < 0) return -1;
+  if (algo == MOAT_GEMM_DOT2 && n > kMaxDot2N) return -1;
+  return plan_gemm(n, k, m, algo, splits).workspace_bytes;
+}
+
+int64_t moat_int4_gemm_workspace_size(int32_t n, int32_t k, int32_t m) {
+  return moat_int4_gemm_ex_workspace_size(n, k, m, MOAT_GEMM_AUTO, 0);
+}
+
+int32_t moat_int4_gemm_ex(const uint16_t* x_f16, const uint8_t* superblocks, float* y_f32, int32_t n, int32_t k,
+                          int32_t m, int32_t algo, int32_t splits, void* workspace, int64_t workspace_bytes,
+                          hipStream_t stream) {
+  if (!gemm_shape_ok(n, k, m) || algo < 0 || algo > 2 || splits < 0) return MOAT_ERR_INVALID;
+  if (!x_f16 || !superblocks || !y_f32) return MOAT_ERR_INVALID;
+  if (!aligned(x_f16, 2) || !aligned(superblocks, 16) || !aligned(y_f32, 4)) return MOAT_ERR_INVALID;
+  const GemmPlan p = plan_gemm(n, k, m, algo, splits);
+  if (p.algo == MOAT_GEMM_DOT2 && n > kMaxDot2N) return MOAT_ERR_INVALID;
+  float* partials = nullptr;
+  uint32_t* counters = nullptr;
+  if (p.splits > 1) {
+    if (!workspace || workspace_bytes < p.workspace_bytes || !aligned(workspace, 16)) return MOAT_ERR_WORKSPACE;
+    counters = static_cast<uint32_t*>(workspace);
+    partials = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + p.counter_bytes);
+  }
+  return status_of(moat::launch_gemm(p.algo, x_f16, superblocks, y_f32, n, k, m, p.splits, partials, counters, stream));
+}
+
+int32_t moat_int4_gemm(const uint16_t* x_f16, const uint8_t* superblocks, float* y_f32, int32_t n, int32_t k,
+                       int32_t m, void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+  return moat_int4_gemm_ex(x_f16, superblocks, y_f32, n, k, m, MOAT_GEMM_AUTO, 0, workspace, workspace_bytes, stream);
+}
+
+int32_t moat_int4_workspace_clear(void* workspace, int64_t bytes, hipStream_t stream) {
+  if (bytes < 0) return MOAT_ERR_INVALID;
+  if (bytes == 0) return MOAT_OK;
+  if (!workspace) return MOAT_ERR_INVALID;
+  return status_of(moat::launch_clear(workspace, bytes, stream));
+}
+
+int32_t moat_int4_quantize(const void* w, int32_t w_dtype, int64_t n, int32_t group_size, int32_t scale_mode,
+                           int8_t* q_out, uint16_t* scales_out, hipStream_t stream) {
+  if (n < 0 || group_size < 1 || (n % group_size) != 0) return MOAT_ERR_INVALID;
+  if (w_dtype != MOAT_DTYPE_F32 && w_dtype != MOAT_DTYPE_F16 && w_dtype != MOAT_DTYPE_F64) return MOAT_ERR_INVALID;
+  if (scale_mode != MOAT_SCALE_F32 && scale_mode != MOAT_SCALE_F16) return MOAT_ERR_INVALID;
+  if (n == 0) return MOAT_OK;
+  if (!w || !q_out || !scales_out) return MOAT_ERR_INVALID;
+  const uintptr_t wa = w_dtype == MOAT_DTYPE_F64 ? 8 : (w_dtype == MOAT_DTYPE_F32 ? 4 : 2);
+  if (!aligned(w, wa) || !aligned(scales_out, 2)) return MOAT_ERR_INVALID;
+  return status_of(moat::launch_quantize(w, w_dtype, n, group_size, scale_mode, q_out, scales_out, stream));
+}
+
+int32_t moat_int4_pack_superblocks(const int8_t* q, const uint16_t* scales_f16, int64_t n_superblocks,
+                                   uint8_t* superblocks_out, hipStream_t stream) {
+  if (n_superblocks < 0) return MOAT_ERR_INVALID;
+  if (n_superblocks == 0) return MOAT_OK;
+  if (!q || !scales_f16 || !superblocks_out) return MOAT_ERR_INVALID;
+  if (!aligned(scales_f16, 2) || !aligned(superblocks_out, 16)) return MOAT_ERR_INVALID;
+  return status_of(moat::launch_pack_superblocks(q, scales_f16, n_superblocks, superblocks_out, stream));
+}
+
+int32_t moat_int4_quantize_pack(const void* w, int32_t w_dtype, int64_t n, int32_t scale_mode,
+                                uint8_t* superblocks_out, hipStream_t stream) {
+  if (n < 0 || (n % 256) != 0) return MOAT_ERR_INVALID;
+  if (w_dtype != MOAT_DTYPE_F32 && w_dtype != MOAT_DTYPE_F16 && w_dtype != MOAT_DTYPE_F64) return MOAT_ERR_INVALID;
+  if (scale_mode != MOAT_SCALE_F32 && scale_mode != MOAT_SCALE_F16) return MOAT_ERR_INVALID;
+  if (n == 0) return MOAT_OK;
+  if (!w || !superblocks_out || !aligned(superblocks_out, 16)) return MOAT_ERR_INVALID;
+  const uintptr_t wa = w_dtype == MOAT_DTYPE_F64 ? 8 : (w_dtype == MOAT_DTYPE_F32 ? 4 : 2);
+  if (!aligned(w, wa)) return MOAT_ERR_INVALID;
+  return status_of(moat::launch_quantize_pack(w, w_dtype, n, scale_mode, superblocks_out, stream));
+}
+
+int32_t moat_int4_pack_nibbles(const int8_t* q, int64_t n, uint8_t* packed_out, hipStream_t stream) {
+  if (n < 0 || (n % 2) != 0) return MOAT_ERR_INVALID;
+  if (n == 0) return MOAT_OK;
+  if (!q || !packed_out) return MOAT_ERR_INVALID;
+  return status_of(moat::launch_pack_nibbles(q, n, packed_out, stream));
+}
+
+int32_t moat_int4_unpack_nibbles(const uint8_t* packed, int64_t n_bytes, int8_t* q_out, hipStream_t stream) {
+  if (n_bytes < 0) return MOAT_ERR_INVALID;
+  if (n_bytes == 0) return MOAT_OK;
+  if (!packed || !q_out) return MOAT_ERR_INVALID;
+  return status_of(moat::launch_unpack_nibbles(packed, n_bytes, q_out, stream));
+}
+
+int32_t moat_int4_group_dequant(const void* q, int32_t q_dtype, const void* scales, int32_t scale_dtype,
+                                int64_t n_groups, int32_t group_size, int32_t table_mode, uint16_t* out_f16,
+                                int32_t* err_flag, hipStream_t stream) {
+  if (n_groups < 0 || group_size < 1 || (table_mode != 0 && table_mode != 1)) return MOAT_ERR_INVALID;
+  if (q_dtype != MOAT_DTYPE_I8 && q_dtype != MOAT_DTYPE_I64 && q_dtype != MOAT_DTYPE_F32) return MOAT_ERR_INVALID;
+  if (table_mode == 1 && q_dtype == MOAT_DTYPE_F32) return MOAT_ERR_INVALID;
+  if (scale_dtype != MOAT_DTYPE_F16 && scale_dtype != MOAT_DTYPE_F32 && scale_dtype != MOAT_DTYPE_F64)
+    return MOAT_ERR_INVALID;
+  if (n_groups == 0) return MOAT_OK;
+  if (!q || !scales || !out_f16 || (table_mode == 1 && !err_flag)) return MOAT_ERR_INVALID;
+  const uintptr_t qa = q_dtype == MOAT_DTYPE_I64 ? 8 : (q_dtype == MOAT_DTYPE_F32 ? 4 : 1);
+  const uintptr_t sa = scale_dtype == MOAT_DTYPE_F64 ? 8 : (scale_dtype == MOAT_DTYPE_F32 ? 4 : 2);
+  if (!aligned(q, qa) || !aligned(scales, sa) || !aligned(out_f16, 2)) return MOAT_ERR_INVALID;
+  return status_of(moat::launch_group_dequant(q, q_dtype, scales, scale_dtype, n_groups, group_size, table_mode,
+                                              out_f16, err_flag, stream));
+}
+
+int32_t moat_int4_lut_gather(const int64_t* q, int64_t n, int32_t index_mode, const uint16_t* lut_f16,
+                             int64_t lut_rows, int32_t lut_len, uint16_t* out_f16, hipStream_t stream) {
+  if (n < 0 || index_mode < 0 || index_mode > 2 || lut_rows < 1 || lut_len < 1) return MOAT_ERR_INVALID;
+  if ((n % lut_rows) != 0) return MOAT_ERR_INVALID;
+  if (n == 0) return MOAT_OK;
+  if (!q || !lut_f16 || !out_f16 || !aligned(q, 8) || !aligned(lut_f16, 2) || !aligned(out_f16, 2))
+    return MOAT_ERR_INVALID;
+  return status_of(moat::launch_lut_gather(q, n, index_mode, lut_f16, lut_rows, lut_len, out_f16, stream));
+}
+
+int32_t moat_int4_any_negative(const int64_t* q, int64_t n, int32_t* flag_out, hipStream_t stream) {
+  if (n < 0 || !flag_out || !aligned(flag_out, 4)) return MOAT_ERR_INVALID;
+  if (n > 0 && (!q || !aligned(q, 8))) return MOAT_ERR_INVALID;
+  return status_of(moat::launch_any_negative(q, n, flag_out, stream));
+}
+
+int32_t moat_int4_to_f16(const void* src, int32_t src_dtype, int64_t n, uint16_t* out_f16, hipStream_t stream) {
+  if (n < 0 || (src_dtype != MOAT_DTYPE_F32 && src_dtype != MOAT_DTYPE_F64)) return MOAT_ERR_INVALID;
+  if (n == 0) return MOAT_OK;
+  if (!src || !out_f16) return MOAT_ERR_INVALID;
+  if (!aligned(src, src_dtype == MOAT_DTYPE_F64 ? 8 : 4) || !aligned(out_f16, 2)) return MOAT_ERR_INVALID;
+  return status_of(moat::launch_to_f16(src, src_dtype, n, out_f16, stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,111 @@
+"""C ABI checks that need no GPU: the library loads, exports every symbol the
+header declares, and rejects bad arguments before touching HIP."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from moat_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "moat_int4.h")
+
+
+def _declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(moat_int4_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.fail("libmoat_int4.so is not built (run `python -m moat_amd.build_lib`)")
+    return _lib.load()
+
+
+def test_every_declared_symbol_is_exported_and_bound(lib):
+    names = _declared_symbols()
+    assert len(names) >= 15
+    for name in names:
+        assert hasattr(lib, name), name
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
+    assert set(_lib.SIGNATURES) == set(names)
+
+
+def test_version_and_status_strings(lib):
+    assert lib.moat_int4_version() == 1
+    assert lib.moat_int4_status_string(0) == b"ok"
+    assert b"invalid" in lib.moat_int4_status_string(-2)
+    assert b"workspace" in lib.moat_int4_status_string(-4)
+
+
+FAKE = ctypes.c_void_p(0x10000)  # never dereferenced: validation fails first
+
+
+@pytest.mark.parametrize("n,k,m", [(0, 256, 256), (33, 256, 256), (1, 256, 48), (1, 3, 32), (1, 0, 256), (1, 256, 16)])
+def test_gemm_rejects_bad_shapes(lib, n, k, m):
+    assert lib.moat_int4_gemm(FAKE, FAKE, FAKE, n, k, m, None, 0, None) == _lib.MOAT_ERR_INVALID
+    assert lib.moat_int4_gemm_workspace_size(n, k, m) == -1
+
+
+def test_gemm_rejects_null_and_misaligned(lib):
+    assert lib.moat_int4_gemm(None, FAKE, FAKE, 1, 256, 256, None, 0, None) == _lib.MOAT_ERR_INVALID
+    assert lib.moat_int4_gemm(FAKE, None, FAKE, 1, 256, 256, None, 0, None) == _lib.MOAT_ERR_INVALID
+    assert lib.moat_int4_gemm(FAKE, FAKE, None, 1, 256, 256, None, 0, None) == _lib.MOAT_ERR_INVALID
+    odd = ctypes.c_void_p(0x10001)
+    assert lib.moat_int4_gemm(odd, FAKE, FAKE, 1, 256, 256, None, 0, None) == _lib.MOAT_ERR_INVALID
+    sb_misaligned = ctypes.c_void_p(0x10008)
+    assert lib.moat_int4_gemm(FAKE, sb_misaligned, FAKE, 1, 256, 256, None, 0, None) == _lib.MOAT_ERR_INVALID
+    # dot2 kernel only up to N = 8
+    assert lib.moat_int4_gemm_ex(FAKE, FAKE, FAKE, 9, 256, 256, _lib.GEMM_DOT2, 1, None, 0, None) == _lib.MOAT_ERR_INVALID
+    assert lib.moat_int4_gemm_ex(FAKE, FAKE, FAKE, 1, 256, 256, 7, 1, None, 0, None) == _lib.MOAT_ERR_INVALID
+
+
+def test_gemm_workspace_contract(lib):
+    # a split-K plan needs a workspace; a missing or short one is refused before launch
+    size = lib.moat_int4_gemm_ex_workspace_size(1, 2048, 5504, _lib.GEMM_MFMA, 8)
+    assert size >= 8 * 1 * 5504 * 4
+    st = lib.moat_int4_gemm_ex(FAKE, FAKE, FAKE, 1, 2048, 5504, _lib.GEMM_MFMA, 8, None, 0, None)
+    assert st == _lib.MOAT_ERR_WORKSPACE
+    st = lib.moat_int4_gemm_ex(FAKE, FAKE, FAKE, 1, 2048, 5504, _lib.GEMM_MFMA, 8, FAKE, size - 1, None)
+    assert st == _lib.MOAT_ERR_WORKSPACE
+    assert lib.moat_int4_gemm_ex_workspace_size(4, 2048, 2048, _lib.GEMM_MFMA, 1) == 0
+    # automatic plans at the benchmark shapes: splits shrink as N grows
+    sizes = [lib.moat_int4_gemm_workspace_size(n, 2048, 5504) for n in (1, 2, 4, 8, 16, 32)]
+    assert all(s >= 0 for s in sizes)
+
+
+def test_other_entry_points_validate(lib):
+    I = _lib.MOAT_ERR_INVALID
+    assert lib.moat_int4_dequant(FAKE, -1, FAKE, None) == I
+    assert lib.moat_int4_dequant(None, 4, FAKE, None) == I
+    assert lib.moat_int4_dequant(ctypes.c_void_p(0x10004), 4, FAKE, None) == I
+    assert lib.moat_int4_dequant(FAKE, 0, FAKE, None) == _lib.MOAT_OK  # nothing to do, no launch
+    assert lib.moat_int4_quantize(FAKE, 0, 33, 32, 0, FAKE, FAKE, None) == I
+    assert lib.moat_int4_quantize(FAKE, 9, 32, 32, 0, FAKE, FAKE, None) == I
+    assert lib.moat_int4_quantize(FAKE, 0, 32, 32, 5, FAKE, FAKE, None) == I
+    assert lib.moat_int4_quantize(FAKE, 0, 32, 0, 0, FAKE, FAKE, None) == I
+    assert lib.moat_int4_quantize_pack(FAKE, 0, 255, 0, FAKE, None) == I
+    assert lib.moat_int4_pack_superblocks(None, FAKE, 1, FAKE, None) == I
+    assert lib.moat_int4_pack_nibbles(FAKE, 3, FAKE, None) == I
+    assert lib.moat_int4_unpack_nibbles(None, 3, FAKE, None) == I
+    assert lib.moat_int4_group_dequant(FAKE, 0, FAKE, 0, 1, 32, 1, FAKE, FAKE, None) == I  # table mode needs ints
+    assert lib.moat_int4_group_dequant(FAKE, 2, FAKE, 2, 1, 32, 0, FAKE, None, None) == I  # int8 scales
+    assert lib.moat_int4_group_dequant(FAKE, 2, FAKE, 1, 1, 32, 1, FAKE, None, None) == I  # no flag in table mode
+    assert lib.moat_int4_lut_gather(FAKE, 10, 0, FAKE, 3, 16, FAKE, None) == I  # 10 % 3
+    assert lib.moat_int4_lut_gather(FAKE, 10, 3, FAKE, 1, 16, FAKE, None) == I
+    assert lib.moat_int4_any_negative(FAKE, 4, None, None) == I
+    assert lib.moat_int4_to_f16(FAKE, 2, 4, FAKE, None) == I
+    assert lib.moat_int4_workspace_clear(None, 16, None) == I
+
+
+def test_product_refuses_to_run_without_gpu():
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    import numpy as np
+    from moat_amd import dequant
+    with pytest.raises(RuntimeError, match="GPU"):
+        dequant.unpack_superblock_weights(np.zeros(144, dtype=np.uint8), 1)
