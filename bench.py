@@ -101,7 +101,8 @@ def main() -> int:
     ap.add_argument("--calls", type=int, default=200, help="timed launches per N for the per-N table")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--graph", action="store_true", help="replay the sweep from a HIP graph")
+    ap.add_argument("--batch", type=int, default=0, help="rounds of loads issued together (0 auto)")
+    ap.add_argument("--finish", type=int, default=0, help="split-K hand-off (0 auto, 1 atomics, 2 fences, 3 kernel)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -136,74 +137,67 @@ def main() -> int:
     xs = {N: torch.from_numpy(np.random.default_rng(2000 + 100 * 2 + N).standard_normal((N, K), dtype=np.float32)
                               .astype(np.float16)).to(dev) for N in ns}
     ys = {N: torch.empty((N, M), dtype=torch.float32, device=dev) for N in ns}
-    stream = torch.cuda.current_stream()
 
     def one_call(N, i):
-        _gemm_into(xs[N], blobs[i % copies], ys[N], K, M, args.algo, args.splits)
+        _gemm_into(xs[N], blobs[i % copies], ys[N], K, M, args.algo, args.splits, args.batch, args.finish)
 
-    counter = [0]
+    # All timed work is replayed from HIP graphs captured on one stream, so the
+    # timed region holds back-to-back kernels and no Python launch overhead.
+    cap = torch.cuda.Stream()
+    cap.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(cap):
+        for N in ns:  # creates this stream's workspace before any capture
+            for i in range(3):
+                one_call(N, i)
+    torch.cuda.synchronize()
 
-    def sweep():
-        for N in ns:
-            one_call(N, counter[0])
-            counter[0] += 1
+    def capture(calls):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=cap):
+            for N, i in calls:
+                one_call(N, i)
+        torch.cuda.synchronize()
+        return g
 
-    # per-N table: back-to-back launches between HIP events on the launch stream
+    def timed(graphs, reps):
+        with torch.cuda.stream(cap):
+            for g in graphs[:2]:
+                g.replay()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(cap)
+            for r in range(reps):
+                graphs[r % len(graphs)].replay()
+            e1.record(cap)
+        e1.synchronize()
+        return e0.elapsed_time(e1) * 1e3  # us
+
+    # per-N table: `calls` launches per N, each on the next weight copy
     per_n = {}
     for N in ns:
-        for i in range(10):
-            one_call(N, i)
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for i in range(args.calls):
-            one_call(N, i)
-        e1.record(stream)
-        e1.synchronize()
-        us = e0.elapsed_time(e1) * 1e3 / args.calls
+        g = capture([(N, i) for i in range(copies)])
+        reps = max(1, args.calls // copies)
+        us = timed([g], reps) / (reps * copies)
         b = algo_bytes(N, K, M)
         per_n[N] = {"us_per_call": round(us, 3), "gbs": round(b / us / 1e3, 1),
                     "roofline_frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4), "tok_s": round(N / us * 1e6, 1),
                     "algo_bytes": b}
         log(f"[bench] N={N:2d}: {us:8.2f} us/call  {b / us / 1e3:7.0f} GB/s  "
             f"{100 * b / us / 1e3 / HBM_PEAK_GBS:5.1f}% of 8 TB/s")
+        del g
     t1 = per_n[ns[0]]["us_per_call"] / ns[0]
     for N in ns:
         per_n[N]["per_token_speedup_vs_first"] = round(t1 / (per_n[N]["us_per_call"] / N), 3)
 
-    graph = None
-    if args.graph:
-        # capture on a stream whose workspace already exists (no allocation or
-        # clearing inside the graph)
-        cap = torch.cuda.Stream()
-        cap.wait_stream(stream)
-        with torch.cuda.stream(cap):
-            for _ in range(3):
-                sweep()
-        torch.cuda.synchronize()
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph, stream=cap):
-            for i, N in enumerate(ns):
-                one_call(N, i)
-        torch.cuda.synchronize()
-
-    def step():
-        if graph is not None:
-            graph.replay()
-        else:
-            sweep()
-
-    for _ in range(args.warmup):
-        step()
+    # steps: one sweep over ns per step; graph s covers steps s, s+G, ... and
+    # every call of every graph reads a different weight copy
+    n_graphs = max(1, copies // len(ns))
+    step_graphs = [capture([(N, s * len(ns) + i) for i, N in enumerate(ns)]) for s in range(n_graphs)]
+    with torch.cuda.stream(cap):
+        for w in range(args.warmup):
+            step_graphs[w % n_graphs].replay()
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for _ in range(args.steps):
-        step()
-    e1.record(stream)
-    e1.synchronize()
-    torch.cuda.synchronize()
-    ms_step = e0.elapsed_time(e1) / args.steps
+    us_total = timed(step_graphs, args.steps)
+    ms_step = us_total / args.steps / 1e3
     tokens = sum(ns)
     value = tokens / (ms_step / 1e3)
     log(f"[bench] sweep: {ms_step * 1e3:.1f} us/step, {value:.0f} tok/s")
@@ -246,8 +240,8 @@ def main() -> int:
         "dtype": "int4-superblock weights, fp16 activations, fp32 accumulate",
         "data": "synthetic",
         "config": {"workload": WORKLOAD_NAMES[args.config], "K": K, "M": M, "ns": ns,
-                   "weight_copies_rotated": copies, "graph": bool(args.graph), "algo": args.algo,
-                   "splits": args.splits},
+                   "weight_copies_rotated": copies, "timing": "HIP graph replay, HIP events on the launch stream",
+                   "algo": args.algo, "splits": args.splits, "batch": args.batch, "finish": args.finish},
         "per_n": {str(k): v for k, v in per_n.items()},
         "roofline": roof,
         "cpu_baseline": cpu,

@@ -82,21 +82,36 @@ int32_t moat_int4_dequant(const uint8_t* superblocks, int64_t n_superblocks,
  * Preconditions: 1 <= n <= 32, k >= 1, m >= 32, m % 32 == 0, (k*m) % 256 == 0;
  * x 2-byte aligned, superblocks 16-byte aligned, y 4-byte aligned.
  * workspace: device memory of moat_int4_gemm_workspace_size() bytes (may be
- * NULL when that size is 0), zero-filled once before first use (e.g. with
- * moat_int4_workspace_clear); every call leaves its counter words at zero
- * again.  Calls that share a workspace must not overlap.
+ * NULL when that size is 0): a fixed 64 KB block of split-K counters followed
+ * by fp32 partials.  Zero-fill it once before first use (e.g. with
+ * moat_int4_workspace_clear); every call leaves the counter block at zero
+ * again, so one workspace serves calls of any shape.  Calls that share a
+ * workspace must not overlap.  m is limited to 2,097,152.
  */
 int64_t moat_int4_gemm_workspace_size(int32_t n, int32_t k, int32_t m);
 int32_t moat_int4_gemm(const uint16_t* x_f16, const uint8_t* superblocks, float* y_f32,
                        int32_t n, int32_t k, int32_t m,
                        void* workspace, int64_t workspace_bytes, hipStream_t stream);
 
-/* Same product with the kernel (MOAT_GEMM_*) and the number of K slices
- * (splits >= 1; 0 = automatic) chosen by the caller: for measurement and for
- * testing each kernel at every n.  Workspace size from the _ex query. */
-int64_t moat_int4_gemm_ex_workspace_size(int32_t n, int32_t k, int32_t m, int32_t algo, int32_t splits);
+/* Launch choices for moat_int4_gemm_ex; zero-initialise for "automatic". */
+typedef struct moat_int4_gemm_options {
+  int32_t algo;   /* MOAT_GEMM_*: 0 automatic, 1 dot2 (n <= 8), 2 MFMA */
+  int32_t splits; /* K slices, >= 1; 0 automatic */
+  int32_t batch;  /* 32-row rounds whose loads a wave issues together: 1, 2 or 4; 0 automatic */
+  int32_t finish; /* split-K hand-off, MOAT_FINISH_*; 0 automatic */
+} moat_int4_gemm_options;
+
+#define MOAT_FINISH_AUTO 0
+#define MOAT_FINISH_DEVICE_ATOMICS 1 /* partials via device-scope atomic stores/loads, one launch */
+#define MOAT_FINISH_FENCES 2         /* partials via plain stores + agent-scope fences, one launch */
+#define MOAT_FINISH_SECOND_KERNEL 3  /* partials via plain stores, summed by a second kernel */
+
+/* Same product with the launch choices made by the caller (NULL = all
+ * automatic): for measurement and for testing each kernel at every n.
+ * Workspace size from the _ex query with the same options. */
+int64_t moat_int4_gemm_ex_workspace_size(int32_t n, int32_t k, int32_t m, const moat_int4_gemm_options* options);
 int32_t moat_int4_gemm_ex(const uint16_t* x_f16, const uint8_t* superblocks, float* y_f32,
-                          int32_t n, int32_t k, int32_t m, int32_t algo, int32_t splits,
+                          int32_t n, int32_t k, int32_t m, const moat_int4_gemm_options* options,
                           void* workspace, int64_t workspace_bytes, hipStream_t stream);
 
 /* Zero `bytes` bytes of device memory with a kernel (no memset node). */

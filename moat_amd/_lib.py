@@ -23,6 +23,13 @@ MOAT_ERR_WORKSPACE = -4
 DTYPE_F32, DTYPE_F16, DTYPE_I8, DTYPE_F64, DTYPE_I64 = 0, 1, 2, 3, 4
 SCALE_F32, SCALE_F16 = 0, 1
 GEMM_AUTO, GEMM_DOT2, GEMM_MFMA = 0, 1, 2
+FINISH_AUTO, FINISH_DEVICE_ATOMICS, FINISH_FENCES, FINISH_SECOND_KERNEL = 0, 1, 2, 3
+
+
+class GemmOptions(ctypes.Structure):
+    """``moat_int4_gemm_options``: zero fields mean automatic."""
+    _fields_ = [("algo", ctypes.c_int32), ("splits", ctypes.c_int32),
+                ("batch", ctypes.c_int32), ("finish", ctypes.c_int32)]
 
 _P = ctypes.c_void_p
 _I32 = ctypes.c_int32
@@ -35,8 +42,8 @@ SIGNATURES = {
     "moat_int4_dequant": (_I32, [_P, _I64, _P, _P]),
     "moat_int4_gemm_workspace_size": (_I64, [_I32, _I32, _I32]),
     "moat_int4_gemm": (_I32, [_P, _P, _P, _I32, _I32, _I32, _P, _I64, _P]),
-    "moat_int4_gemm_ex_workspace_size": (_I64, [_I32, _I32, _I32, _I32, _I32]),
-    "moat_int4_gemm_ex": (_I32, [_P, _P, _P, _I32, _I32, _I32, _I32, _I32, _P, _I64, _P]),
+    "moat_int4_gemm_ex_workspace_size": (_I64, [_I32, _I32, _I32, ctypes.POINTER(GemmOptions)]),
+    "moat_int4_gemm_ex": (_I32, [_P, _P, _P, _I32, _I32, _I32, ctypes.POINTER(GemmOptions), _P, _I64, _P]),
     "moat_int4_workspace_clear": (_I32, [_P, _I64, _P]),
     "moat_int4_quantize": (_I32, [_P, _I32, _I64, _I32, _I32, _P, _P, _P]),
     "moat_int4_pack_superblocks": (_I32, [_P, _P, _I64, _P, _P]),

@@ -25,14 +25,18 @@ hipError_t launch_quantize_pack(const void* w, int dtype, int64_t n, int scale_m
 int gemm_col_tiles(int m);
 int gemm_rounds(int k);
 hipError_t launch_gemm(int algo, const uint16_t* x, const uint8_t* sb, float* y, int n, int k, int m, int splits,
-                       float* partials, uint32_t* counters, hipStream_t stream);
+                       int batch, int finish, float* partials, uint32_t* counters, hipStream_t stream);
 }  // namespace moat
 
 namespace {
 
 constexpr int kMaxN = 32;
 constexpr int kMaxDot2N = 8;
-constexpr int64_t kCounterAlign = 256;
+// The split-K counters live in a fixed block at the start of the workspace so
+// that no call's partials (which follow the block) can overlap the counter
+// words of a call with more column tiles: 16384 tiles = M up to 2,097,152.
+constexpr int64_t kCounterBlockBytes = 64 * 1024;
+constexpr int kMaxColTiles = (int)(kCounterBlockBytes / 4);
 
 bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 
@@ -41,6 +45,8 @@ int32_t status_of(hipError_t e) { return e == hipSuccess ? MOAT_OK : MOAT_ERR_HI
 struct GemmPlan {
   int algo;
   int splits;
+  int batch;
+  int finish;  // kernel-side FinishMode: 0 device atomics, 1 fences, 2 second kernel
   int64_t counter_bytes;
   int64_t workspace_bytes;
 };
@@ -50,6 +56,16 @@ bool gemm_shape_ok(int32_t n, int32_t k, int32_t m) {
   if (((int64_t)k * (int64_t)m) % 256 != 0) return false;
   // byte offsets of one 32-row round are 32-bit in the kernels
   if ((int64_t)m * 33 * 18 > (int64_t)0xFFFFFFFF) return false;
+  if (moat::gemm_col_tiles(m) > kMaxColTiles) return false;
+  return true;
+}
+
+bool options_ok(const moat_int4_gemm_options* o, int32_t n) {
+  if (!o) return true;
+  if (o->algo < 0 || o->algo > 2 || o->splits < 0) return false;
+  if (o->batch != 0 && o->batch != 1 && o->batch != 2 && o->batch != 4) return false;
+  if (o->finish < 0 || o->finish > 3) return false;
+  if (o->algo == MOAT_GEMM_DOT2 && n > kMaxDot2N) return false;
   return true;
 }
 
@@ -58,12 +74,14 @@ bool gemm_shape_ok(int32_t n, int32_t k, int32_t m) {
 // idle at these sizes) against partial-sum traffic, which is
 // splits * N * M * 8 bytes against 0.5625 * K * M bytes of weights; it is kept
 // below a quarter of the weight stream.
-GemmPlan plan_gemm(int32_t n, int32_t k, int32_t m, int32_t algo, int32_t splits) {
+GemmPlan plan_gemm(int32_t n, int32_t k, int32_t m, const moat_int4_gemm_options* o) {
+  moat_int4_gemm_options opt = {0, 0, 0, 0};
+  if (o) opt = *o;
   GemmPlan p;
-  if (algo == MOAT_GEMM_AUTO) algo = (n <= 2) ? MOAT_GEMM_DOT2 : MOAT_GEMM_MFMA;
-  p.algo = algo;
+  p.algo = opt.algo == MOAT_GEMM_AUTO ? ((n <= 2) ? MOAT_GEMM_DOT2 : MOAT_GEMM_MFMA) : opt.algo;
   const int tiles = moat::gemm_col_tiles(m);
   const int rounds = moat::gemm_rounds(k);
+  int splits = opt.splits;
   if (splits <= 0) {
     const int target_wgs = 640;
     int s = (target_wgs + tiles / 2) / tiles;
@@ -77,8 +95,12 @@ GemmPlan plan_gemm(int32_t n, int32_t k, int32_t m, int32_t algo, int32_t splits
   }
   if (splits > rounds) splits = rounds;
   p.splits = splits;
+  // rounds per wave in this plan; a wave issues up to 4 rounds of loads at once
+  const int per_wave = (rounds + 4 * splits - 1) / (4 * splits);
+  p.batch = opt.batch ? opt.batch : (per_wave >= 4 ? 4 : (per_wave >= 2 ? 2 : 1));
+  p.finish = opt.finish ? opt.finish - 1 : 0;
   if (splits > 1) {
-    p.counter_bytes = ((int64_t)tiles * 4 + kCounterAlign - 1) / kCounterAlign * kCounterAlign;
+    p.counter_bytes = kCounterBlockBytes;
     p.workspace_bytes = p.counter_bytes + (int64_t)splits * n * m * 4;
   } else {
     p.counter_bytes = 0;
@@ -110,23 +132,22 @@ int32_t moat_int4_dequant(const uint8_t* superblocks, int64_t n_superblocks, uin
   return status_of(moat::launch_dequant_stream(superblocks, n_superblocks, out_f16, stream));
 }
 
-int64_t moat_int4_gemm_ex_workspace_size(int32_t n, int32_t k, int32_t m, int32_t algo, int32_t splits) {
-  if (!gemm_shape_ok(n, k, m) || algo < 0 || algo > 2 || splits < 0) return -1;
-  if (algo == MOAT_GEMM_DOT2 && n > kMaxDot2N) return -1;
-  return plan_gemm(n, k, m, algo, splits).workspace_bytes;
+int64_t moat_int4_gemm_ex_workspace_size(int32_t n, int32_t k, int32_t m, const moat_int4_gemm_options* options) {
+  if (!gemm_shape_ok(n, k, m) || !options_ok(options, n)) return -1;
+  return plan_gemm(n, k, m, options).workspace_bytes;
 }
 
 int64_t moat_int4_gemm_workspace_size(int32_t n, int32_t k, int32_t m) {
-  return moat_int4_gemm_ex_workspace_size(n, k, m, MOAT_GEMM_AUTO, 0);
+  return moat_int4_gemm_ex_workspace_size(n, k, m, nullptr);
 }
 
 int32_t moat_int4_gemm_ex(const uint16_t* x_f16, const uint8_t* superblocks, float* y_f32, int32_t n, int32_t k,
-                          int32_t m, int32_t algo, int32_t splits, void* workspace, int64_t workspace_bytes,
+                          int32_t m, const moat_int4_gemm_options* options, void* workspace, int64_t workspace_bytes,
                           hipStream_t stream) {
-  if (!gemm_shape_ok(n, k, m) || algo < 0 || algo > 2 || splits < 0) return MOAT_ERR_INVALID;
+  if (!gemm_shape_ok(n, k, m) || !options_ok(options, n)) return MOAT_ERR_INVALID;
   if (!x_f16 || !superblocks || !y_f32) return MOAT_ERR_INVALID;
   if (!aligned(x_f16, 2) || !aligned(superblocks, 16) || !aligned(y_f32, 4)) return MOAT_ERR_INVALID;
-  const GemmPlan p = plan_gemm(n, k, m, algo, splits);
+  const GemmPlan p = plan_gemm(n, k, m, options);
   if (p.algo == MOAT_GEMM_DOT2 && n > kMaxDot2N) return MOAT_ERR_INVALID;
   float* partials = nullptr;
   uint32_t* counters = nullptr;
@@ -135,12 +156,13 @@ int32_t moat_int4_gemm_ex(const uint16_t* x_f16, const uint8_t* superblocks, flo
     counters = static_cast<uint32_t*>(workspace);
     partials = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + p.counter_bytes);
   }
-  return status_of(moat::launch_gemm(p.algo, x_f16, superblocks, y_f32, n, k, m, p.splits, partials, counters, stream));
+  return status_of(moat::launch_gemm(p.algo, x_f16, superblocks, y_f32, n, k, m, p.splits, p.batch, p.finish, partials,
+                                     counters, stream));
 }
 
 int32_t moat_int4_gemm(const uint16_t* x_f16, const uint8_t* superblocks, float* y_f32, int32_t n, int32_t k,
                        int32_t m, void* workspace, int64_t workspace_bytes, hipStream_t stream) {
-  return moat_int4_gemm_ex(x_f16, superblocks, y_f32, n, k, m, MOAT_GEMM_AUTO, 0, workspace, workspace_bytes, stream);
+  return moat_int4_gemm_ex(x_f16, superblocks, y_f32, n, k, m, nullptr, workspace, workspace_bytes, stream);
 }
 
 int32_t moat_int4_workspace_clear(void* workspace, int64_t bytes, hipStream_t stream) {

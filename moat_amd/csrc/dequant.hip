@@ -84,7 +84,12 @@ __global__ void __launch_bounds__(256) group_dequant_kernel(const QT* __restrict
       }
       v = (float)((idx < 0 ? idx + 16 : idx) - 8);
     }
-    const _Float16 h = (_Float16)(v * s);
+    float prod = v * s;
+    // Materialise the float32 product: without this the compiler folds the
+    // multiply and the fp16 conversion into one v_fma_mixlo_f16, which rounds
+    // once instead of twice and differs from the reference for float32 scales.
+    asm volatile("" : "+v"(prod));
+    const _Float16 h = (_Float16)prod;
     out[i] = __builtin_bit_cast(uint16_t, h);
   }
 }

@@ -15,20 +15,27 @@
 //    dword of one group per row, and lane group q owns rows 8q..8q+7 of each
 //    32-row "round";
 //  * per round a lane issues 8 dword loads (its 8 rows) and 8 fp16 scale
-//    loads; for 16 lanes of a lane group those dwords are 64 contiguous
-//    payload bytes of one row, so the wave reads 4 rows x 64 B per load;
+//    loads; for the 16 lanes of a lane group those dwords are 64 contiguous
+//    payload bytes of one row;
+//  * a wave takes every 4th round of its workgroup's slice and issues the
+//    loads of kBatch rounds before using any of them, so that a short slice
+//    costs one memory latency rather than one latency per round;
 //  * the nibbles are turned into (row t, row t+1) fp16 pairs per column
 //    (v_perm_b32 + the magic-exponent trick + v_pk_mul by the scale pair);
 //    for a column c the four pairs are exactly the 8-deep K slice a lane
 //    contributes to a v_mfma_f32_16x16x32_f16 B operand (kk = 8q + t);
-//  * MFMA variant: A operand = X[n][32r + 8q .. +7] for n = lane j (one
+//  * MFMA kernel: A operand = X[n][32r + 8q .. +7] for n = lane j (one
 //    16-byte load), one MFMA per column c and 16-row block of X;
-//  * DOT2 variant (no matrix cores): v_dot2_f32_f16 of each pair with the
+//  * DOT2 kernel (no matrix cores): v_dot2_f32_f16 of each pair with the
 //    matching X pair, then a shuffle reduction across the 4 lane groups;
-//  * the 4 waves of a workgroup take interleaved rounds and are summed through
-//    two LDS slots (32 KB at N = 32); with K split over `splits` workgroups, each writes an fp32 partial
-//    and the last one to finish a column tile (device-scope counter) adds the
-//    partials in split order, so results are deterministic.
+//  * the 4 waves of a workgroup are summed through two LDS slots (32 KB at
+//    N = 32); with K split over `splits` workgroups, each publishes an fp32
+//    partial and the last one to finish a column tile adds the partials in
+//    split order, so results are deterministic;
+//  * workgroup ids are remapped so that each XCD (ids are dealt round-robin
+//    to the 8 XCDs) works on one contiguous range of (split, tile) pairs:
+//    neighbouring column tiles share 128-byte lines, which then meet in the
+//    same L2.
 #include "superblock_device.h"
 
 namespace moat {
@@ -37,6 +44,19 @@ constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * 64;
 constexpr int kTileCols = 128;
 constexpr int kRoundRows = 32;
+constexpr int kXcds = 8;
+
+// How a split-K workgroup hands its partial to the last one of its tile.
+enum FinishMode : int {
+  // partials written and read with device-scope atomic (sc1) accesses; the
+  // writer waits for its stores to complete before the counter increment.
+  kFinishDeviceAtomics = 0,
+  // plain stores + agent-scope release/acquire fences (whole-L2 writeback
+  // and invalidate in every workgroup)
+  kFinishFences = 1,
+  // plain stores only; a second kernel adds the partials
+  kFinishSecondKernel = 2,
+};
 
 struct GemmParams {
   const uint16_t* x;       // [N][K] fp16
@@ -47,7 +67,9 @@ struct GemmParams {
   int n, k, m;
   int splits;
   int rounds;              // ceil(k / 32)
+  int tiles;               // ceil(m / 128)
   int x_vec;               // x is 16-byte aligned and k % 8 == 0: 16-byte X loads
+  int finish;              // FinishMode
 };
 
 // Per-lane loads for one 32-row round.
@@ -56,20 +78,27 @@ struct RoundData {
   uint32_t s[4];   // fp16 scales of rows (2p, 2p+1) packed lo/hi
 };
 
-template <bool kMasked>
 __device__ __forceinline__ void load_round(RoundData& d, const uint8_t* __restrict__ sb, uint64_t round_off,
                                            const uint32_t (&poff)[8], const uint32_t (&soff)[8],
-                                           uint32_t scale_mask, int row0, int k) {
+                                           uint32_t scale_mask, int row0, int k, bool masked) {
   const uint8_t* base = sb + round_off;
   uint32_t sc[8];
+  if (!masked) {
 #pragma unroll
-  for (int t = 0; t < 8; ++t) {
-    if (!kMasked || row0 + t < k) {
+    for (int t = 0; t < 8; ++t) {
       d.w[t] = *reinterpret_cast<const uint32_t*>(base + poff[t]);
       sc[t] = *reinterpret_cast<const uint16_t*>(base + soff[t]);
-    } else {
-      d.w[t] = 0x88888888u;  // every nibble is 8, i.e. value 0
-      sc[t] = 0;
+    }
+  } else {
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      if (row0 + t < k) {
+        d.w[t] = *reinterpret_cast<const uint32_t*>(base + poff[t]);
+        sc[t] = *reinterpret_cast<const uint16_t*>(base + soff[t]);
+      } else {
+        d.w[t] = 0x88888888u;  // every nibble is 8, i.e. value 0
+        sc[t] = 0;
+      }
     }
   }
 #pragma unroll
@@ -93,12 +122,7 @@ __device__ __forceinline__ half8_t load_x8(const uint16_t* __restrict__ x, int n
 }
 
 template <int NT>
-struct MfmaAcc {
-  float4_t c[NT][8];
-};
-
-template <int NT>
-__device__ __forceinline__ void mfma_round(MfmaAcc<NT>& acc, const RoundData& d, const half8_t (&xa)[NT]) {
+__device__ __forceinline__ void mfma_round(float4_t (&acc)[NT][8], const RoundData& d, const half8_t (&xa)[NT]) {
   half2_t pr[4][8];
 #pragma unroll
   for (int p = 0; p < 4; ++p) dequant_row_pair(d.w[2 * p], d.w[2 * p + 1], bitcast<half2_t>(d.s[p]), pr[p]);
@@ -111,7 +135,7 @@ __device__ __forceinline__ void mfma_round(MfmaAcc<NT>& acc, const RoundData& d,
     b[6] = pr[3][c][0]; b[7] = pr[3][c][1];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-      acc.c[nt][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[nt], b, acc.c[nt][c], 0, 0, 0);
+      acc[nt][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[nt], b, acc[nt][c], 0, 0, 0);
     }
   }
 }
@@ -132,7 +156,7 @@ __device__ __forceinline__ void dot2_round(float (&acc)[NN][8], const RoundData&
 }
 
 // Two LDS slots hold the tile: waves 2 and 3 store, then waves 0 and 1 add
-// (wave w < 2 adds into slot w).  Each lane touches the same positions in
+// (wave w adds into slot w & 1).  Each lane touches the same positions in
 // both phases.
 __device__ __forceinline__ void tile_put(float* red, int per_wave, int wave, int idx, float v, bool phase_add) {
   float* slot = red + (wave & 1) * per_wave;
@@ -140,8 +164,19 @@ __device__ __forceinline__ void tile_put(float* red, int per_wave, int wave, int
   else slot[idx] = v;
 }
 
-// Sum the two LDS slots, then store to Y (one split) or to the
-// partial buffer followed by the last-arriver reduction.
+__device__ __forceinline__ void store_partial(float* p, float v, int finish) {
+  if (finish == kFinishDeviceAtomics) __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else *p = v;
+}
+
+__device__ __forceinline__ float load_partial(const float* p, int finish) {
+  if (finish == kFinishDeviceAtomics)
+    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return *p;
+}
+
+// Sum the two LDS slots, then store to Y (one split) or publish the partial;
+// the last workgroup of the tile to publish adds all partials in split order.
 __device__ __forceinline__ void finish_tile(const GemmParams& P, float* red, int npad, int tile, int split) {
   const int tid = threadIdx.x;
   const int ncols = kTileCols;
@@ -151,8 +186,7 @@ __device__ __forceinline__ void finish_tile(const GemmParams& P, float* red, int
     for (int idx = tid; idx < P.n * ncols; idx += kThreads) {
       const int n = idx / ncols, c = idx % ncols;
       if (m0 + c >= P.m) continue;
-      const float v = red[n * ncols + c] + red[per_wave + n * ncols + c];
-      P.y[(int64_t)n * P.m + m0 + c] = v;
+      P.y[(int64_t)n * P.m + m0 + c] = red[n * ncols + c] + red[per_wave + n * ncols + c];
     }
     return;
   }
@@ -160,33 +194,39 @@ __device__ __forceinline__ void finish_tile(const GemmParams& P, float* red, int
   for (int idx = tid; idx < P.n * ncols; idx += kThreads) {
     const int n = idx / ncols, c = idx % ncols;
     if (m0 + c >= P.m) continue;
-    const float v = red[n * ncols + c] + red[per_wave + n * ncols + c];
-    part[(int64_t)n * P.m + m0 + c] = v;
+    store_partial(&part[(int64_t)n * P.m + m0 + c], red[n * ncols + c] + red[per_wave + n * ncols + c], P.finish);
   }
+  if (P.finish == kFinishSecondKernel) return;
   __shared__ int s_last;
-  __threadfence();
+  if (P.finish == kFinishFences) {
+    __threadfence();
+  } else {
+    // the device-scope stores above must have completed before the counter moves
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_s_waitcnt(0);
+  }
   __syncthreads();
   if (tid == 0) {
-    const uint32_t prev = atomicAdd(&P.counters[tile], 1u);
+    const uint32_t prev = __hip_atomic_fetch_add(&P.counters[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     s_last = (prev == (uint32_t)(P.splits - 1));
   }
   __syncthreads();
   if (!s_last) return;
-  __threadfence();
+  if (P.finish == kFinishFences) __threadfence();
   for (int idx = tid; idx < P.n * ncols; idx += kThreads) {
     const int n = idx / ncols, c = idx % ncols;
     if (m0 + c >= P.m) continue;
     const int64_t o = (int64_t)n * P.m + m0 + c;
     float v = 0.0f;
-    for (int s = 0; s < P.splits; ++s) {
-      v += __builtin_nontemporal_load(&P.partials[(int64_t)s * P.n * P.m + o]);
-    }
+    for (int s = 0; s < P.splits; ++s) v += load_partial(&P.partials[(int64_t)s * P.n * P.m + o], P.finish);
     P.y[o] = v;
   }
-  if (tid == 0) atomicExch(&P.counters[tile], 0u);
+  if (tid == 0) __hip_atomic_store(&P.counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Per-lane byte offsets of its 8 rows in round 0 (row = 8q + t).
+// Per-lane byte offsets of its 8 rows in round 0 (row = 8q + t).  Moving
+// down 32 rows adds 32*M/32 = M groups; M % 8 == 0 keeps (g & 7) unchanged,
+// so every later round is the same offsets plus 18*M bytes per round.
 __device__ __forceinline__ void lane_offsets(uint32_t (&poff)[8], uint32_t (&soff)[8], int q, int mcol, int m) {
   const uint32_t gpr = (uint32_t)(m >> 5);  // groups per row
   const uint32_t gcol = (uint32_t)(mcol >> 5);
@@ -199,12 +239,26 @@ __device__ __forceinline__ void lane_offsets(uint32_t (&poff)[8], uint32_t (&sof
   }
 }
 
-template <int NT>
+// blockIdx.x -> (tile, split): ids b and b+8 run on the same XCD, so deal
+// contiguous logical ranges to each XCD; the logical index is split-major,
+// keeping neighbouring tiles of one K slice together.
+__device__ __forceinline__ void block_coords(const GemmParams& P, int& tile, int& split) {
+  const int total = P.tiles * P.splits;
+  const int b = blockIdx.x;
+  const int per = total / kXcds;
+  int logical = b;
+  if (b < per * kXcds) logical = (b % kXcds) * per + b / kXcds;
+  split = logical / P.tiles;
+  tile = logical % P.tiles;
+}
+
+template <int NT, int kBatch>
 __global__ void __launch_bounds__(kThreads) int4_gemm_mfma_kernel(GemmParams P) {
   extern __shared__ float red[];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int j = lane & 15, q = lane >> 4;
-  const int tile = blockIdx.x, split = blockIdx.y;
+  int tile, split;
+  block_coords(P, tile, split);
   const int mcol = tile * kTileCols + 8 * j;
   const bool col_ok = mcol < P.m;
   uint32_t poff[8], soff[8];
@@ -216,33 +270,30 @@ __global__ void __launch_bounds__(kThreads) int4_gemm_mfma_kernel(GemmParams P) 
   const int r_end = (int)((int64_t)(split + 1) * P.rounds / P.splits);
   const bool xfast_ok = P.x_vec != 0;
 
-  MfmaAcc<NT> acc;
+  float4_t acc[NT][8];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-    for (int c = 0; c < 8; ++c) acc.c[nt][c] = float4_t{0.f, 0.f, 0.f, 0.f};
+    for (int c = 0; c < 8; ++c) acc[nt][c] = float4_t{0.f, 0.f, 0.f, 0.f};
 
-  RoundData cur, nxt;
-  int r = r_begin + wave;
-  if (r < r_end) {
-    const int row0 = r * kRoundRows + 8 * q;
-    if ((r + 1) * kRoundRows <= P.k) load_round<false>(cur, P.sb, r * round_bytes, poff, soff, smask, row0, P.k);
-    else load_round<true>(cur, P.sb, r * round_bytes, poff, soff, smask, row0, P.k);
-  }
-  for (; r < r_end; r += kWaves) {
-    const int rn = r + kWaves;
-    if (rn < r_end) {
-      const int row0n = rn * kRoundRows + 8 * q;
-      if ((rn + 1) * kRoundRows <= P.k) load_round<false>(nxt, P.sb, rn * round_bytes, poff, soff, smask, row0n, P.k);
-      else load_round<true>(nxt, P.sb, rn * round_bytes, poff, soff, smask, row0n, P.k);
-    }
-    const int kk = r * kRoundRows + 8 * q;
-    const bool xfast = xfast_ok && (kk + 8 <= P.k);
-    half8_t xa[NT];
+  for (int rb = r_begin + wave; rb < r_end; rb += kWaves * kBatch) {
+    RoundData d[kBatch];
+    half8_t xa[kBatch][NT];
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) xa[nt] = load_x8(P.x, nt * 16 + j, P.n, kk, P.k, xfast);
-    mfma_round<NT>(acc, cur, xa);
-    cur = nxt;
+    for (int i = 0; i < kBatch; ++i) {
+      const int r = rb + i * kWaves;
+      if (r < r_end) {
+        const int row0 = r * kRoundRows + 8 * q;
+        load_round(d[i], P.sb, r * round_bytes, poff, soff, smask, row0, P.k, (r + 1) * kRoundRows > P.k);
+        const bool xfast = xfast_ok && (row0 + 8 <= P.k);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) xa[i][nt] = load_x8(P.x, nt * 16 + j, P.n, row0, P.k, xfast);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      if (rb + i * kWaves < r_end) mfma_round<NT>(acc, d[i], xa[i]);
+    }
   }
 
   // D layout of v_mfma_f32_16x16x32_f16: lane (q, j) holds rows 4q..4q+3, column j.
@@ -257,19 +308,20 @@ __global__ void __launch_bounds__(kThreads) int4_gemm_mfma_kernel(GemmParams P) 
         for (int c = 0; c < 8; ++c)
 #pragma unroll
           for (int v = 0; v < 4; ++v)
-            tile_put(red, per_wave, wave, (nt * 16 + 4 * q + v) * kTileCols + 8 * j + c, acc.c[nt][c][v], phase == 1);
+            tile_put(red, per_wave, wave, (nt * 16 + 4 * q + v) * kTileCols + 8 * j + c, acc[nt][c][v], phase == 1);
     }
     __syncthreads();
   }
   finish_tile(P, red, npad, tile, split);
 }
 
-template <int NN>
+template <int NN, int kBatch>
 __global__ void __launch_bounds__(kThreads) int4_gemm_dot2_kernel(GemmParams P) {
   extern __shared__ float red[];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int j = lane & 15, q = lane >> 4;
-  const int tile = blockIdx.x, split = blockIdx.y;
+  int tile, split;
+  block_coords(P, tile, split);
   const int mcol = tile * kTileCols + 8 * j;
   const bool col_ok = mcol < P.m;
   uint32_t poff[8], soff[8];
@@ -286,27 +338,24 @@ __global__ void __launch_bounds__(kThreads) int4_gemm_dot2_kernel(GemmParams P) 
 #pragma unroll
     for (int c = 0; c < 8; ++c) acc[nn][c] = 0.0f;
 
-  RoundData cur, nxt;
-  int r = r_begin + wave;
-  if (r < r_end) {
-    const int row0 = r * kRoundRows + 8 * q;
-    if ((r + 1) * kRoundRows <= P.k) load_round<false>(cur, P.sb, r * round_bytes, poff, soff, smask, row0, P.k);
-    else load_round<true>(cur, P.sb, r * round_bytes, poff, soff, smask, row0, P.k);
-  }
-  for (; r < r_end; r += kWaves) {
-    const int rn = r + kWaves;
-    if (rn < r_end) {
-      const int row0n = rn * kRoundRows + 8 * q;
-      if ((rn + 1) * kRoundRows <= P.k) load_round<false>(nxt, P.sb, rn * round_bytes, poff, soff, smask, row0n, P.k);
-      else load_round<true>(nxt, P.sb, rn * round_bytes, poff, soff, smask, row0n, P.k);
-    }
-    const int kk = r * kRoundRows + 8 * q;
-    const bool xfast = xfast_ok && (kk + 8 <= P.k);
-    half8_t xr[NN];
+  for (int rb = r_begin + wave; rb < r_end; rb += kWaves * kBatch) {
+    RoundData d[kBatch];
+    half8_t xr[kBatch][NN];
 #pragma unroll
-    for (int nn = 0; nn < NN; ++nn) xr[nn] = load_x8(P.x, nn, P.n, kk, P.k, xfast);
-    dot2_round<NN>(acc, cur, xr);
-    cur = nxt;
+    for (int i = 0; i < kBatch; ++i) {
+      const int r = rb + i * kWaves;
+      if (r < r_end) {
+        const int row0 = r * kRoundRows + 8 * q;
+        load_round(d[i], P.sb, r * round_bytes, poff, soff, smask, row0, P.k, (r + 1) * kRoundRows > P.k);
+        const bool xfast = xfast_ok && (row0 + 8 <= P.k);
+#pragma unroll
+        for (int nn = 0; nn < NN; ++nn) xr[i][nn] = load_x8(P.x, nn, P.n, row0, P.k, xfast);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      if (rb + i * kWaves < r_end) dot2_round<NN>(acc, d[i], xr[i]);
+    }
   }
 
   // wavefront reduction over the 4 lane groups (lanes j, j+16, j+32, j+48)
@@ -334,45 +383,63 @@ __global__ void __launch_bounds__(kThreads) int4_gemm_dot2_kernel(GemmParams P) 
   finish_tile(P, red, npad, tile, split);
 }
 
-}  // namespace moat
+// Second kernel of kFinishSecondKernel: y = sum over splits of the partials.
+__global__ void __launch_bounds__(256) splitk_sum_kernel(const float* __restrict__ partials, int splits,
+                                                         int64_t nm, float* __restrict__ y) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nm; i += stride) {
+    float v = 0.0f;
+    for (int s = 0; s < splits; ++s) v += partials[(int64_t)s * nm + i];
+    y[i] = v;
+  }
+}
 
 // ---------------------------------------------------------------------------
-// Host-side launch (called from abi.cpp after argument validation).
-
-namespace moat {
+// Host-side launch (called from abi.hip after argument validation).
 
 int gemm_col_tiles(int m) { return (m + kTileCols - 1) / kTileCols; }
 int gemm_rounds(int k) { return (k + kRoundRows - 1) / kRoundRows; }
 
-hipError_t launch_gemm(int algo, const uint16_t* x, const uint8_t* sb, float* y, int n, int k, int m,
-                       int splits, float* partials, uint32_t* counters, hipStream_t stream) {
+template <int B>
+static hipError_t launch_gemm_batch(const GemmParams& P, int algo, hipStream_t stream) {
+  dim3 grid(P.tiles * P.splits), block(kThreads);
+  if (algo == 2) {
+    if (P.n <= 16) {
+      hipLaunchKernelGGL((int4_gemm_mfma_kernel<1, B>), grid, block, (size_t)2 * 16 * kTileCols * 4, stream, P);
+    } else {
+      hipLaunchKernelGGL((int4_gemm_mfma_kernel<2, B>), grid, block, (size_t)2 * 32 * kTileCols * 4, stream, P);
+    }
+    return hipGetLastError();
+  }
+  switch (P.n) {
+#define MOAT_DOT2_CASE(NNV)                                                                               \
+  case NNV:                                                                                               \
+    hipLaunchKernelGGL((int4_gemm_dot2_kernel<NNV, B>), grid, block, (size_t)2 * NNV * kTileCols * 4, stream, P); \
+    break;
+    MOAT_DOT2_CASE(1) MOAT_DOT2_CASE(2) MOAT_DOT2_CASE(3) MOAT_DOT2_CASE(4)
+    MOAT_DOT2_CASE(5) MOAT_DOT2_CASE(6) MOAT_DOT2_CASE(7) MOAT_DOT2_CASE(8)
+#undef MOAT_DOT2_CASE
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_gemm(int algo, const uint16_t* x, const uint8_t* sb, float* y, int n, int k, int m, int splits,
+                       int batch, int finish, float* partials, uint32_t* counters, hipStream_t stream) {
   GemmParams P;
   P.x = x; P.sb = sb; P.y = y; P.partials = partials; P.counters = counters;
-  P.n = n; P.k = k; P.m = m; P.splits = splits; P.rounds = gemm_rounds(k);
+  P.n = n; P.k = k; P.m = m; P.splits = splits; P.rounds = gemm_rounds(k); P.tiles = gemm_col_tiles(m);
   P.x_vec = ((reinterpret_cast<uintptr_t>(x) & 15) == 0 && (k % 8) == 0) ? 1 : 0;
-  dim3 grid(gemm_col_tiles(m), splits), block(kThreads);
-  if (algo == 2) {
-    if (n <= 16) {
-      const size_t lds = (size_t)2 * 16 * kTileCols * sizeof(float);
-      hipLaunchKernelGGL(int4_gemm_mfma_kernel<1>, grid, block, lds, stream, P);
-    } else {
-      const size_t lds = (size_t)2 * 32 * kTileCols * sizeof(float);
-      hipLaunchKernelGGL(int4_gemm_mfma_kernel<2>, grid, block, lds, stream, P);
-    }
-  } else {
-#define MOAT_DOT2_CASE(NNV)                                                               \
-  case NNV: {                                                                             \
-    const size_t lds = (size_t)2 * NNV * kTileCols * sizeof(float);                  \
-    hipLaunchKernelGGL(int4_gemm_dot2_kernel<NNV>, grid, block, lds, stream, P);           \
-    break;                                                                                \
-  }
-    switch (n) {
-      MOAT_DOT2_CASE(1) MOAT_DOT2_CASE(2) MOAT_DOT2_CASE(3) MOAT_DOT2_CASE(4)
-      MOAT_DOT2_CASE(5) MOAT_DOT2_CASE(6) MOAT_DOT2_CASE(7) MOAT_DOT2_CASE(8)
-      default: return hipErrorInvalidValue;
-    }
-#undef MOAT_DOT2_CASE
-  }
+  P.finish = finish;
+  hipError_t e;
+  if (batch >= 4) e = launch_gemm_batch<4>(P, algo, stream);
+  else if (batch == 2) e = launch_gemm_batch<2>(P, algo, stream);
+  else e = launch_gemm_batch<1>(P, algo, stream);
+  if (e != hipSuccess || splits == 1 || finish != kFinishSecondKernel) return e;
+  const int64_t nm = (int64_t)n * m;
+  int64_t blocks = (nm + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  hipLaunchKernelGGL(splitk_sum_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, partials, splits, nm, y);
   return hipGetLastError();
 }
 

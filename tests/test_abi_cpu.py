@@ -34,6 +34,22 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
     assert set(_lib.SIGNATURES) == set(names)
 
 
+def _declared_arities():
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    out = {}
+    for name, args in re.findall(r"\b(moat_int4_\w+)\s*\(([^)]*)\)\s*;", text):
+        args = args.strip()
+        out[name] = 0 if args in ("", "void") else args.count(",") + 1
+    return out
+
+
+def test_bindings_match_header_arity():
+    arities = _declared_arities()
+    assert set(arities) == set(_lib.SIGNATURES)
+    for name, n in arities.items():
+        assert len(_lib.SIGNATURES[name][1]) == n, name
+
+
 def test_version_and_status_strings(lib):
     assert lib.moat_int4_version() == 1
     assert lib.moat_int4_status_string(0) == b"ok"
@@ -58,20 +74,27 @@ def test_gemm_rejects_null_and_misaligned(lib):
     assert lib.moat_int4_gemm(odd, FAKE, FAKE, 1, 256, 256, None, 0, None) == _lib.MOAT_ERR_INVALID
     sb_misaligned = ctypes.c_void_p(0x10008)
     assert lib.moat_int4_gemm(FAKE, sb_misaligned, FAKE, 1, 256, 256, None, 0, None) == _lib.MOAT_ERR_INVALID
-    # dot2 kernel only up to N = 8
-    assert lib.moat_int4_gemm_ex(FAKE, FAKE, FAKE, 9, 256, 256, _lib.GEMM_DOT2, 1, None, 0, None) == _lib.MOAT_ERR_INVALID
-    assert lib.moat_int4_gemm_ex(FAKE, FAKE, FAKE, 1, 256, 256, 7, 1, None, 0, None) == _lib.MOAT_ERR_INVALID
+    # dot2 kernel only up to N = 8; unknown algo / batch / finish values are refused
+    for opt in (_lib.GemmOptions(_lib.GEMM_DOT2, 1, 0, 0),):
+        assert lib.moat_int4_gemm_ex(FAKE, FAKE, FAKE, 9, 256, 256, ctypes.byref(opt), None, 0, None) == _lib.MOAT_ERR_INVALID
+    for opt in (_lib.GemmOptions(7, 1, 0, 0), _lib.GemmOptions(0, 1, 3, 0), _lib.GemmOptions(0, 1, 0, 4),
+                _lib.GemmOptions(0, -1, 0, 0)):
+        assert lib.moat_int4_gemm_ex(FAKE, FAKE, FAKE, 1, 256, 256, ctypes.byref(opt), None, 0, None) == _lib.MOAT_ERR_INVALID
+        assert lib.moat_int4_gemm_ex_workspace_size(1, 256, 256, ctypes.byref(opt)) == -1
 
 
 def test_gemm_workspace_contract(lib):
     # a split-K plan needs a workspace; a missing or short one is refused before launch
-    size = lib.moat_int4_gemm_ex_workspace_size(1, 2048, 5504, _lib.GEMM_MFMA, 8)
-    assert size >= 8 * 1 * 5504 * 4
-    st = lib.moat_int4_gemm_ex(FAKE, FAKE, FAKE, 1, 2048, 5504, _lib.GEMM_MFMA, 8, None, 0, None)
+    opt = _lib.GemmOptions(_lib.GEMM_MFMA, 8, 0, 0)
+    size = lib.moat_int4_gemm_ex_workspace_size(1, 2048, 5504, ctypes.byref(opt))
+    assert size == 64 * 1024 + 8 * 1 * 5504 * 4  # fixed counter block + partials
+    st = lib.moat_int4_gemm_ex(FAKE, FAKE, FAKE, 1, 2048, 5504, ctypes.byref(opt), None, 0, None)
     assert st == _lib.MOAT_ERR_WORKSPACE
-    st = lib.moat_int4_gemm_ex(FAKE, FAKE, FAKE, 1, 2048, 5504, _lib.GEMM_MFMA, 8, FAKE, size - 1, None)
+    st = lib.moat_int4_gemm_ex(FAKE, FAKE, FAKE, 1, 2048, 5504, ctypes.byref(opt), FAKE, size - 1, None)
     assert st == _lib.MOAT_ERR_WORKSPACE
-    assert lib.moat_int4_gemm_ex_workspace_size(4, 2048, 2048, _lib.GEMM_MFMA, 1) == 0
+    one = _lib.GemmOptions(_lib.GEMM_MFMA, 1, 0, 0)
+    assert lib.moat_int4_gemm_ex_workspace_size(4, 2048, 2048, ctypes.byref(one)) == 0
+    assert lib.moat_int4_gemm_ex_workspace_size(4, 2048, 2048, None) >= 0
     # automatic plans at the benchmark shapes: splits shrink as N grows
     sizes = [lib.moat_int4_gemm_workspace_size(n, 2048, 5504) for n in (1, 2, 4, 8, 16, 32)]
     assert all(s >= 0 for s in sizes)

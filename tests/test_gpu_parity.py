@@ -140,11 +140,11 @@ def test_gemm_matches_oracle_all_kernels(name, ns):
         xd = torch.from_numpy(x).cuda()
         algos = [L.GEMM_AUTO, L.GEMM_MFMA] + ([L.GEMM_DOT2] if N <= 8 else [])
         for algo in algos:
-            for splits in (0, 1, 3):
-                say(f"case: gemm {name} N={N} algo={algo} splits={splits}")
-                y = batched_int4_matmul(xd, blob_d, K, M, algo=algo, splits=splits)
+            for splits, batch, finish in ((0, 0, 0), (1, 0, 0), (3, 1, 1), (3, 2, 2), (7, 4, 3)):
+                say(f"case: gemm {name} N={N} algo={algo} splits={splits} batch={batch} finish={finish}")
+                y = batched_int4_matmul(xd, blob_d, K, M, algo=algo, splits=splits, batch=batch, finish=finish)
                 e = rel_err(y.cpu().numpy(), yref)
-                assert e <= TOL, (name, N, algo, splits, e)
+                assert e <= TOL, (name, N, algo, splits, batch, finish, e)
 
 
 def test_gemm_equals_stacked_gemv():
@@ -172,9 +172,10 @@ def test_gemm_runner_stream_closed_form():
     x = np.ones((8, K), dtype=np.float16)
     for algo in (L.GEMM_MFMA, L.GEMM_DOT2):
         for splits in (1, 4, 16):
-            say(f"case: runner stream algo={algo} splits={splits}")
-            y = batched_int4_matmul(x, blob, K, M, algo=algo, splits=splits)
-            assert np.all(y == np.float32(-0.5 * K)), (algo, splits)
+            for finish in (1, 2, 3):
+                say(f"case: runner stream algo={algo} splits={splits} finish={finish}")
+                y = batched_int4_matmul(x, blob, K, M, algo=algo, splits=splits, finish=finish)
+                assert np.all(y == np.float32(-0.5 * K)), (algo, splits, finish)
 
 
 @pytest.mark.parametrize("K,M", [(3, 256), (64, 160), (12, 64), (40, 96), (256, 32), (1000, 224)])
@@ -191,10 +192,10 @@ def test_gemm_ragged_shapes(K, M):
         for algo in (L.GEMM_MFMA, L.GEMM_DOT2):
             if algo == L.GEMM_DOT2 and N > 8:
                 continue
-            for splits in (1, 2):
-                say(f"case: ragged K={K} M={M} N={N} algo={algo} splits={splits}")
-                y = batched_int4_matmul(x, blob, K, M, algo=algo, splits=splits)
-                assert rel_err(y, yref) <= TOL, (K, M, N, algo, splits)
+            for splits, batch in ((1, 1), (2, 2), (2, 4)):
+                say(f"case: ragged K={K} M={M} N={N} algo={algo} splits={splits} batch={batch}")
+                y = batched_int4_matmul(x, blob, K, M, algo=algo, splits=splits, batch=batch)
+                assert rel_err(y, yref) <= TOL, (K, M, N, algo, splits, batch)
 
 
 def test_gemm_unaligned_activations_and_zero_rows():
@@ -213,15 +214,20 @@ def test_gemm_unaligned_activations_and_zero_rows():
     assert np.all(z == 0)
 
 
-def test_gemm_deterministic_across_calls():
+def test_gemm_split_k_handoff_is_deterministic():
+    """Every split-K hand-off gives the same bits on every call (partials are
+    added in split order), and the hand-offs agree with each other."""
     from moat_amd.dequant import batched_int4_matmul
     K, M, _, blob = workload("cfg2 2048x5504")
     blob_d = torch.from_numpy(blob.reshape(-1)).cuda()
-    x = torch.from_numpy(_x(4, K, 3)).cuda()
-    a = batched_int4_matmul(x, blob_d, K, M, splits=12)
-    for _ in range(3):
-        b = batched_int4_matmul(x, blob_d, K, M, splits=12)
-        assert torch.equal(a, b)
+    for N in (1, 4, 32):
+        x = torch.from_numpy(_x(N, K, 3)).cuda()
+        ref = batched_int4_matmul(x, blob_d, K, M, algo=2, splits=16, finish=3)
+        for finish in (1, 2, 3):
+            say(f"case: split-K hand-off N={N} finish={finish}")
+            for _ in range(20):
+                y = batched_int4_matmul(x, blob_d, K, M, algo=2, splits=16, finish=finish)
+                assert torch.equal(y, ref), (N, finish)
 
 
 def test_gemm_n_above_32_is_sliced():
