@@ -99,12 +99,17 @@ typedef struct moat_int4_gemm_options {
   int32_t splits; /* K slices, >= 1; 0 automatic */
   int32_t batch;  /* 32-row rounds whose loads a wave issues together: 1, 2 or 4; 0 automatic */
   int32_t finish; /* split-K hand-off, MOAT_FINISH_*; 0 automatic */
+  int32_t front;  /* weight loads, MOAT_FRONT_*; 0 automatic */
 } moat_int4_gemm_options;
 
 #define MOAT_FINISH_AUTO 0
 #define MOAT_FINISH_DEVICE_ATOMICS 1 /* partials via device-scope atomic stores/loads, one launch */
 #define MOAT_FINISH_FENCES 2         /* partials via plain stores + agent-scope fences, one launch */
 #define MOAT_FINISH_SECOND_KERNEL 3  /* partials via plain stores, summed by a second kernel */
+
+#define MOAT_FRONT_AUTO 0
+#define MOAT_FRONT_LDS 1    /* global_load_lds staging (m % 64 == 0; otherwise direct) */
+#define MOAT_FRONT_DIRECT 2 /* 4-byte loads straight into registers */
 
 /* Same product with the launch choices made by the caller (NULL = all
  * automatic): for measurement and for testing each kernel at every n.

@@ -14,9 +14,16 @@
 //    slice of its rows; lane j owns columns 8j..8j+7 of the tile, i.e. one
 //    dword of one group per row, and lane group q owns rows 8q..8q+7 of each
 //    32-row "round";
-//  * per round a lane issues 8 dword loads (its 8 rows) and 8 fp16 scale
-//    loads; for the 16 lanes of a lane group those dwords are 64 contiguous
-//    payload bytes of one row;
+//  * staged path (M % 64 == 0): per round a wave copies its 32 rows x 4
+//    group chunks (2 KB of payload) and the 4 scales of each row (256 B)
+//    straight from HBM into LDS with three global_load_lds instructions
+//    (dwordx4 / dword per lane), then reads its MFMA operand layout back with
+//    one ds_read_b32 per row: the load slots are ordered so that lane l's
+//    dword of row t sits at byte 256*t + 4*l, which makes every read one
+//    contiguous, conflict-free 256-byte LDS access.  Few, wide memory
+//    instructions keep enough bytes in flight per CU to approach the HBM
+//    rate; 4-byte loads straight into registers (the direct path, kept for
+//    other M) cap far lower;
 //  * a wave takes every 4th round of its workgroup's slice and issues the
 //    loads of kBatch rounds before using any of them, so that a short slice
 //    costs one memory latency rather than one latency per round;
@@ -252,6 +259,226 @@ __device__ __forceinline__ void block_coords(const GemmParams& P, int& tile, int
   tile = logical % P.tiles;
 }
 
+// ---------------------------------------------------------------------------
+// LDS-staged front end.
+
+constexpr int kStagePayload = 2048;  // 32 rows x 4 group chunks x 16 B
+constexpr int kStageRound = kStagePayload + 256;  // + 32 rows x 4 fp16 scales
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// Per-lane source offsets (round 0) of its three load slots:
+//  payload slot s = 64*i + lane (i = 0, 1) holds row 8*((s>>2)&3) + (s>>4),
+//  group (s & 3) of the tile; scale slot u = lane holds the fp16 pair of
+//  groups (2*(u&1), 2*(u&1)+1) of row u >> 1.
+struct StageOffsets {
+  uint32_t pay[2];
+  uint32_t sc;
+  bool pay_ok[2];  // group inside the matrix (ragged last tile)
+  bool sc_ok;
+  int pay_row[2];  // row inside the round
+  int sc_row;
+};
+
+__device__ __forceinline__ void stage_offsets(StageOffsets& o, int lane, int tile, int m) {
+  const uint32_t gpr = (uint32_t)(m >> 5);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int s = 64 * i + lane;
+    const int row = 8 * ((s >> 2) & 3) + (s >> 4);
+    const uint32_t gcol = (uint32_t)(4 * tile + (s & 3));
+    const uint32_t g = (uint32_t)row * gpr + gcol;
+    o.pay[i] = (g >> 3) * kSbBytes + kSbHeader + ((g & 7) << 4);
+    o.pay_ok[i] = gcol < gpr;
+    o.pay_row[i] = row;
+  }
+  const int row = lane >> 1;
+  const uint32_t gcol = (uint32_t)(4 * tile + 2 * (lane & 1));
+  const uint32_t g = (uint32_t)row * gpr + gcol;  // even when M % 64 == 0, so the pair is 4-byte aligned
+  o.sc = (g >> 3) * kSbBytes + ((g & 7) << 1);
+  o.sc_ok = gcol < gpr;
+  o.sc_row = row;
+}
+
+// Issue the three LDS copies of one round (rows >= k are not loaded).
+__device__ __forceinline__ void stage_round(const StageOffsets& o, const uint8_t* __restrict__ sb, uint64_t round_off,
+                                            int round_row0, int k, uint8_t* dst) {
+  const uint8_t* base = sb + round_off;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    if (o.pay_ok[i] && round_row0 + o.pay_row[i] < k)
+      __builtin_amdgcn_global_load_lds((const void*)(base + o.pay[i]), (lds_ptr_t)(dst + 1024 * i), 16, 0, 0);
+  }
+  if (o.sc_ok && round_row0 + o.sc_row < k)
+    __builtin_amdgcn_global_load_lds((const void*)(base + o.sc), (lds_ptr_t)(dst + kStagePayload), 4, 0, 0);
+}
+
+// Read one round back in the register layout of RoundData.  Rows >= k and
+// columns outside the matrix get scale 0 (their LDS bytes are stale, and
+// every nibble times 0 is 0).
+__device__ __forceinline__ void read_round(RoundData& d, const uint8_t* src, int lane, int q, int a, int round_row0,
+                                           int k, uint32_t scale_mask) {
+#pragma unroll
+  for (int t = 0; t < 8; ++t) d.w[t] = *reinterpret_cast<const uint32_t*>(src + 256 * t + 4 * lane);
+  const uint8_t* sc = src + kStagePayload + 2 * a;
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const int r0 = 8 * q + 2 * p;
+    uint32_t lo = *reinterpret_cast<const uint16_t*>(sc + 8 * r0);
+    uint32_t hi = *reinterpret_cast<const uint16_t*>(sc + 8 * (r0 + 1));
+    if (round_row0 + r0 >= k) lo = 0;
+    if (round_row0 + r0 + 1 >= k) hi = 0;
+    d.s[p] = (lo | (hi << 16)) & scale_mask;
+  }
+}
+
+template <int NT, int kBatch>
+__global__ void __launch_bounds__(kThreads) int4_gemm_mfma_staged_kernel(GemmParams P) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int j = lane & 15, q = lane >> 4, a = j >> 2;
+  int tile, split;
+  block_coords(P, tile, split);
+  const bool col_ok = tile * kTileCols + 8 * j < P.m;
+  const uint32_t smask = col_ok ? 0xFFFFFFFFu : 0u;
+  StageOffsets so;
+  stage_offsets(so, lane, tile, P.m);
+  const uint64_t round_bytes = (uint64_t)18 * (uint64_t)P.m;
+  const int r_begin = (int)((int64_t)split * P.rounds / P.splits);
+  const int r_end = (int)((int64_t)(split + 1) * P.rounds / P.splits);
+  const bool xfast_ok = P.x_vec != 0;
+  uint8_t* stage = smem + wave * kBatch * kStageRound;
+
+  float4_t acc[NT][8];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+    for (int c = 0; c < 8; ++c) acc[nt][c] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+  for (int rb = r_begin + wave; rb < r_end; rb += kWaves * kBatch) {
+    half8_t xa[kBatch][NT];
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      const int r = rb + i * kWaves;
+      if (r < r_end) {
+        stage_round(so, P.sb, r * round_bytes, r * kRoundRows, P.k, stage + i * kStageRound);
+        const int row0 = r * kRoundRows + 8 * q;
+        const bool xfast = xfast_ok && (row0 + 8 <= P.k);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) xa[i][nt] = load_x8(P.x, nt * 16 + j, P.n, row0, P.k, xfast);
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // the LDS copies of this batch have landed
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      const int r = rb + i * kWaves;
+      if (r < r_end) {
+        RoundData d;
+        read_round(d, stage + i * kStageRound, lane, q, a, r * kRoundRows, P.k, smask);
+        mfma_round<NT>(acc, d, xa[i]);
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // reads done before the next batch overwrites the stage
+  }
+  __syncthreads();  // the stage area is reused for the tile reduction
+
+  float* red = reinterpret_cast<float*>(smem);
+  const int npad = NT * 16;
+  const int per_wave = npad * kTileCols;
+#pragma unroll
+  for (int phase = 0; phase < 2; ++phase) {
+    if ((wave >> 1) == 1 - phase) {
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
+#pragma unroll
+          for (int v = 0; v < 4; ++v)
+            tile_put(red, per_wave, wave, (nt * 16 + 4 * q + v) * kTileCols + 8 * j + c, acc[nt][c][v], phase == 1);
+    }
+    __syncthreads();
+  }
+  finish_tile(P, red, npad, tile, split);
+}
+
+template <int NN, int kBatch>
+__global__ void __launch_bounds__(kThreads) int4_gemm_dot2_staged_kernel(GemmParams P) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int j = lane & 15, q = lane >> 4, a = j >> 2;
+  int tile, split;
+  block_coords(P, tile, split);
+  const bool col_ok = tile * kTileCols + 8 * j < P.m;
+  const uint32_t smask = col_ok ? 0xFFFFFFFFu : 0u;
+  StageOffsets so;
+  stage_offsets(so, lane, tile, P.m);
+  const uint64_t round_bytes = (uint64_t)18 * (uint64_t)P.m;
+  const int r_begin = (int)((int64_t)split * P.rounds / P.splits);
+  const int r_end = (int)((int64_t)(split + 1) * P.rounds / P.splits);
+  const bool xfast_ok = P.x_vec != 0;
+  uint8_t* stage = smem + wave * kBatch * kStageRound;
+
+  float acc[NN][8];
+#pragma unroll
+  for (int nn = 0; nn < NN; ++nn)
+#pragma unroll
+    for (int c = 0; c < 8; ++c) acc[nn][c] = 0.0f;
+
+  for (int rb = r_begin + wave; rb < r_end; rb += kWaves * kBatch) {
+    half8_t xr[kBatch][NN];
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      const int r = rb + i * kWaves;
+      if (r < r_end) {
+        stage_round(so, P.sb, r * round_bytes, r * kRoundRows, P.k, stage + i * kStageRound);
+        const int row0 = r * kRoundRows + 8 * q;
+        const bool xfast = xfast_ok && (row0 + 8 <= P.k);
+#pragma unroll
+        for (int nn = 0; nn < NN; ++nn) xr[i][nn] = load_x8(P.x, nn, P.n, row0, P.k, xfast);
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      const int r = rb + i * kWaves;
+      if (r < r_end) {
+        RoundData d;
+        read_round(d, stage + i * kStageRound, lane, q, a, r * kRoundRows, P.k, smask);
+        dot2_round<NN>(acc, d, xr[i]);
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+  }
+  __syncthreads();
+
+#pragma unroll
+  for (int nn = 0; nn < NN; ++nn)
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      float v = acc[nn][c];
+      v += __shfl_xor(v, 16);
+      v += __shfl_xor(v, 32);
+      acc[nn][c] = v;
+    }
+  float* red = reinterpret_cast<float*>(smem);
+  const int npad = NN;
+  const int per_wave = npad * kTileCols;
+#pragma unroll
+  for (int phase = 0; phase < 2; ++phase) {
+    if ((wave >> 1) == 1 - phase && q == 0) {
+#pragma unroll
+      for (int nn = 0; nn < NN; ++nn)
+#pragma unroll
+        for (int c = 0; c < 8; ++c) tile_put(red, per_wave, wave, nn * kTileCols + 8 * j + c, acc[nn][c], phase == 1);
+    }
+    __syncthreads();
+  }
+  finish_tile(P, red, npad, tile, split);
+}
+
+// ---------------------------------------------------------------------------
+// Direct front end (any M % 32 == 0): 4-byte loads straight into registers.
+
 template <int NT, int kBatch>
 __global__ void __launch_bounds__(kThreads) int4_gemm_mfma_kernel(GemmParams P) {
   extern __shared__ float red[];
@@ -400,21 +627,28 @@ __global__ void __launch_bounds__(256) splitk_sum_kernel(const float* __restrict
 int gemm_col_tiles(int m) { return (m + kTileCols - 1) / kTileCols; }
 int gemm_rounds(int k) { return (k + kRoundRows - 1) / kRoundRows; }
 
+static size_t reduce_lds(int npad) { return (size_t)2 * npad * kTileCols * sizeof(float); }
+
 template <int B>
-static hipError_t launch_gemm_batch(const GemmParams& P, int algo, hipStream_t stream) {
+static hipError_t launch_gemm_batch(const GemmParams& P, int algo, bool staged, hipStream_t stream) {
   dim3 grid(P.tiles * P.splits), block(kThreads);
+  const size_t stage_lds = (size_t)kWaves * B * kStageRound;
+  auto lds_for = [&](int npad) { return staged ? (stage_lds > reduce_lds(npad) ? stage_lds : reduce_lds(npad)) : reduce_lds(npad); };
   if (algo == 2) {
     if (P.n <= 16) {
-      hipLaunchKernelGGL((int4_gemm_mfma_kernel<1, B>), grid, block, (size_t)2 * 16 * kTileCols * 4, stream, P);
+      if (staged) hipLaunchKernelGGL((int4_gemm_mfma_staged_kernel<1, B>), grid, block, lds_for(16), stream, P);
+      else hipLaunchKernelGGL((int4_gemm_mfma_kernel<1, B>), grid, block, lds_for(16), stream, P);
     } else {
-      hipLaunchKernelGGL((int4_gemm_mfma_kernel<2, B>), grid, block, (size_t)2 * 32 * kTileCols * 4, stream, P);
+      if (staged) hipLaunchKernelGGL((int4_gemm_mfma_staged_kernel<2, B>), grid, block, lds_for(32), stream, P);
+      else hipLaunchKernelGGL((int4_gemm_mfma_kernel<2, B>), grid, block, lds_for(32), stream, P);
     }
     return hipGetLastError();
   }
   switch (P.n) {
-#define MOAT_DOT2_CASE(NNV)                                                                               \
-  case NNV:                                                                                               \
-    hipLaunchKernelGGL((int4_gemm_dot2_kernel<NNV, B>), grid, block, (size_t)2 * NNV * kTileCols * 4, stream, P); \
+#define MOAT_DOT2_CASE(NNV)                                                                                  \
+  case NNV:                                                                                                  \
+    if (staged) hipLaunchKernelGGL((int4_gemm_dot2_staged_kernel<NNV, B>), grid, block, lds_for(NNV), stream, P); \
+    else hipLaunchKernelGGL((int4_gemm_dot2_kernel<NNV, B>), grid, block, lds_for(NNV), stream, P);          \
     break;
     MOAT_DOT2_CASE(1) MOAT_DOT2_CASE(2) MOAT_DOT2_CASE(3) MOAT_DOT2_CASE(4)
     MOAT_DOT2_CASE(5) MOAT_DOT2_CASE(6) MOAT_DOT2_CASE(7) MOAT_DOT2_CASE(8)
@@ -425,16 +659,17 @@ static hipError_t launch_gemm_batch(const GemmParams& P, int algo, hipStream_t s
 }
 
 hipError_t launch_gemm(int algo, const uint16_t* x, const uint8_t* sb, float* y, int n, int k, int m, int splits,
-                       int batch, int finish, float* partials, uint32_t* counters, hipStream_t stream) {
+                       int batch, int finish, int staged, float* partials, uint32_t* counters, hipStream_t stream) {
   GemmParams P;
   P.x = x; P.sb = sb; P.y = y; P.partials = partials; P.counters = counters;
   P.n = n; P.k = k; P.m = m; P.splits = splits; P.rounds = gemm_rounds(k); P.tiles = gemm_col_tiles(m);
   P.x_vec = ((reinterpret_cast<uintptr_t>(x) & 15) == 0 && (k % 8) == 0) ? 1 : 0;
   P.finish = finish;
+  const bool st = staged != 0 && (m % 64) == 0;
   hipError_t e;
-  if (batch >= 4) e = launch_gemm_batch<4>(P, algo, stream);
-  else if (batch == 2) e = launch_gemm_batch<2>(P, algo, stream);
-  else e = launch_gemm_batch<1>(P, algo, stream);
+  if (batch >= 4) e = launch_gemm_batch<4>(P, algo, st, stream);
+  else if (batch == 2) e = launch_gemm_batch<2>(P, algo, st, stream);
+  else e = launch_gemm_batch<1>(P, algo, st, stream);
   if (e != hipSuccess || splits == 1 || finish != kFinishSecondKernel) return e;
   const int64_t nm = (int64_t)n * m;
   int64_t blocks = (nm + 255) / 256;

@@ -140,11 +140,13 @@ def test_gemm_matches_oracle_all_kernels(name, ns):
         xd = torch.from_numpy(x).cuda()
         algos = [L.GEMM_AUTO, L.GEMM_MFMA] + ([L.GEMM_DOT2] if N <= 8 else [])
         for algo in algos:
-            for splits, batch, finish in ((0, 0, 0), (1, 0, 0), (3, 1, 1), (3, 2, 2), (7, 4, 3)):
-                say(f"case: gemm {name} N={N} algo={algo} splits={splits} batch={batch} finish={finish}")
-                y = batched_int4_matmul(xd, blob_d, K, M, algo=algo, splits=splits, batch=batch, finish=finish)
+            for splits, batch, finish, front in ((0, 0, 0, 0), (1, 0, 0, 1), (1, 0, 0, 2), (3, 1, 1, 1), (3, 2, 2, 2),
+                                                 (7, 4, 3, 1), (5, 4, 1, 2)):
+                say(f"case: gemm {name} N={N} algo={algo} splits={splits} batch={batch} finish={finish} front={front}")
+                y = batched_int4_matmul(xd, blob_d, K, M, algo=algo, splits=splits, batch=batch, finish=finish,
+                                        front=front)
                 e = rel_err(y.cpu().numpy(), yref)
-                assert e <= TOL, (name, N, algo, splits, batch, finish, e)
+                assert e <= TOL, (name, N, algo, splits, batch, finish, front, e)
 
 
 def test_gemm_equals_stacked_gemv():
@@ -178,7 +180,8 @@ def test_gemm_runner_stream_closed_form():
                 assert np.all(y == np.float32(-0.5 * K)), (algo, splits, finish)
 
 
-@pytest.mark.parametrize("K,M", [(3, 256), (64, 160), (12, 64), (40, 96), (256, 32), (1000, 224)])
+@pytest.mark.parametrize("K,M", [(3, 256), (64, 160), (12, 64), (40, 96), (256, 32), (1000, 224), (24, 192),
+                                 (100, 448)])
 def test_gemm_ragged_shapes(K, M):
     """K not a multiple of 32 or 8, M not a multiple of the 128-column tile."""
     from moat_amd.dequant import batched_int4_matmul
@@ -192,10 +195,10 @@ def test_gemm_ragged_shapes(K, M):
         for algo in (L.GEMM_MFMA, L.GEMM_DOT2):
             if algo == L.GEMM_DOT2 and N > 8:
                 continue
-            for splits, batch in ((1, 1), (2, 2), (2, 4)):
-                say(f"case: ragged K={K} M={M} N={N} algo={algo} splits={splits} batch={batch}")
-                y = batched_int4_matmul(x, blob, K, M, algo=algo, splits=splits, batch=batch)
-                assert rel_err(y, yref) <= TOL, (K, M, N, algo, splits, batch)
+            for splits, batch, front in ((1, 1, 1), (2, 2, 1), (2, 4, 1), (1, 1, 2), (2, 4, 2)):
+                say(f"case: ragged K={K} M={M} N={N} algo={algo} splits={splits} batch={batch} front={front}")
+                y = batched_int4_matmul(x, blob, K, M, algo=algo, splits=splits, batch=batch, front=front)
+                assert rel_err(y, yref) <= TOL, (K, M, N, algo, splits, batch, front)
 
 
 def test_gemm_unaligned_activations_and_zero_rows():
