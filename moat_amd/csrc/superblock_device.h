@@ -44,13 +44,26 @@ __device__ __forceinline__ uint32_t bits(half2_t v) { return __builtin_bit_cast(
 constexpr uint32_t kMagicLo = 0x64006400u;  // 1024 in both halves
 constexpr uint32_t kMagicHi = 0x54005400u;  // 64 in both halves
 
-__device__ __forceinline__ half2_t nib_lo_pair(uint32_t p) {  // nibbles in bits 0-3 and 16-19
+// The magic words can be passed in from VGPRs: with one mask constant in an
+// SGPR and the magic in a VGPR, (p & mask) | magic is a single v_and_or_b32
+// (GFX9 VOP3 takes no literal and one scalar operand).
+__device__ __forceinline__ half2_t nib_lo_pair(uint32_t p, uint32_t magic = kMagicLo) {  // bits 0-3 and 16-19
   const half2_t off = {(_Float16)1032.0f, (_Float16)1032.0f};
-  return bitcast<half2_t>((p & 0x000F000Fu) | kMagicLo) - off;
+  return bitcast<half2_t>((p & 0x000F000Fu) | magic) - off;
 }
-__device__ __forceinline__ half2_t nib_hi_pair(uint32_t p) {  // nibbles in bits 4-7 and 20-23
+__device__ __forceinline__ half2_t nib_hi_pair(uint32_t p, uint32_t magic = kMagicHi) {  // bits 4-7 and 20-23
   const half2_t off = {(_Float16)72.0f, (_Float16)72.0f};
-  return bitcast<half2_t>((p & 0x00F000F0u) | kMagicHi) - off;
+  return bitcast<half2_t>((p & 0x00F000F0u) | magic) - off;
+}
+
+// The two magic words as opaque VGPR values (see nib_lo_pair).
+struct MagicWords {
+  uint32_t lo, hi;
+};
+__device__ __forceinline__ MagicWords magic_words() {
+  MagicWords m{kMagicLo, kMagicHi};
+  asm volatile("" : "+v"(m.lo), "+v"(m.hi));
+  return m;
 }
 
 // v_perm_b32: result byte i = byte sel_i of the 8-byte value {hi: s0, lo: s1};
@@ -77,17 +90,18 @@ __device__ __forceinline__ void dequant_dword_in_order(uint32_t v, half2_t sc, h
 
 // Two dwords of the same 8 columns in consecutive rows (a = row t, b = row
 // t+1) -> 8 half2, out[c] = (W[t][c], W[t+1][c]) for column c = 0..7.
-__device__ __forceinline__ void dequant_row_pair(uint32_t a, uint32_t b, half2_t sc, half2_t out[8]) {
-  uint32_t p0 = byte_pair<0>(a, b), p1 = byte_pair<1>(a, b);
-  uint32_t p2 = byte_pair<2>(a, b), p3 = byte_pair<3>(a, b);
-  out[0] = nib_lo_pair(p0) * sc;
-  out[1] = nib_hi_pair(p0) * sc;
-  out[2] = nib_lo_pair(p1) * sc;
-  out[3] = nib_hi_pair(p1) * sc;
-  out[4] = nib_lo_pair(p2) * sc;
-  out[5] = nib_hi_pair(p2) * sc;
-  out[6] = nib_lo_pair(p3) * sc;
-  out[7] = nib_hi_pair(p3) * sc;
+__device__ __forceinline__ void dequant_row_pair(uint32_t a, uint32_t b, half2_t sc, half2_t out[8],
+                                                 MagicWords mw = MagicWords{kMagicLo, kMagicHi}) {
+  const uint32_t p0 = byte_pair<0>(a, b), p1 = byte_pair<1>(a, b);
+  const uint32_t p2 = byte_pair<2>(a, b), p3 = byte_pair<3>(a, b);
+  out[0] = nib_lo_pair(p0, mw.lo) * sc;
+  out[1] = nib_hi_pair(p0, mw.hi) * sc;
+  out[2] = nib_lo_pair(p1, mw.lo) * sc;
+  out[3] = nib_hi_pair(p1, mw.hi) * sc;
+  out[4] = nib_lo_pair(p2, mw.lo) * sc;
+  out[5] = nib_hi_pair(p2, mw.hi) * sc;
+  out[6] = nib_lo_pair(p3, mw.lo) * sc;
+  out[7] = nib_hi_pair(p3, mw.hi) * sc;
 }
 
 }  // namespace moat

@@ -181,7 +181,7 @@ def test_gemm_runner_stream_closed_form():
 
 
 @pytest.mark.parametrize("K,M", [(3, 256), (64, 160), (12, 64), (40, 96), (256, 32), (1000, 224), (24, 192),
-                                 (100, 448)])
+                                 (100, 448), (293, 256), (1000, 448), (518, 128)])
 def test_gemm_ragged_shapes(K, M):
     """K not a multiple of 32 or 8, M not a multiple of the 128-column tile."""
     from moat_amd.dequant import batched_int4_matmul
