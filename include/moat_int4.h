@@ -108,8 +108,9 @@ typedef struct moat_int4_gemm_options {
 #define MOAT_FINISH_SECOND_KERNEL 3  /* partials via plain stores, summed by a second kernel */
 
 #define MOAT_FRONT_AUTO 0
-#define MOAT_FRONT_LDS 1    /* global_load_lds staging (m % 64 == 0; otherwise direct) */
-#define MOAT_FRONT_DIRECT 2 /* 4-byte loads straight into registers */
+#define MOAT_FRONT_LDS 1     /* 16-byte vector loads staged through LDS (m % 64 == 0; otherwise direct) */
+#define MOAT_FRONT_DIRECT 2  /* 4-byte loads straight into registers */
+#define MOAT_FRONT_LDS_DMA 3 /* global_load_lds staging (m % 64 == 0; otherwise direct) */
 
 /* Same product with the launch choices made by the caller (NULL = all
  * automatic): for measurement and for testing each kernel at every n.

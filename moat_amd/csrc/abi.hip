@@ -25,7 +25,7 @@ hipError_t launch_quantize_pack(const void* w, int dtype, int64_t n, int scale_m
 int gemm_col_tiles(int m);
 int gemm_rounds(int k);
 hipError_t launch_gemm(int algo, const uint16_t* x, const uint8_t* sb, float* y, int n, int k, int m, int splits,
-                       int batch, int finish, int staged, float* partials, uint32_t* counters, hipStream_t stream);
+                       int batch, int finish, int front, float* partials, uint32_t* counters, hipStream_t stream);
 }  // namespace moat
 
 namespace {
@@ -47,7 +47,7 @@ struct GemmPlan {
   int splits;
   int batch;
   int finish;  // kernel-side FinishMode: 0 device atomics, 1 fences, 2 second kernel
-  int staged;  // LDS-staged front end (used when m % 64 == 0)
+  int front;   // kernel-side front end: 0 direct, 1 LDS DMA, 2 vector loads + LDS
   int64_t counter_bytes;
   int64_t workspace_bytes;
 };
@@ -66,7 +66,7 @@ bool options_ok(const moat_int4_gemm_options* o, int32_t n) {
   if (o->algo < 0 || o->algo > 2 || o->splits < 0) return false;
   if (o->batch != 0 && o->batch != 1 && o->batch != 2 && o->batch != 4) return false;
   if (o->finish < 0 || o->finish > 3) return false;
-  if (o->front < 0 || o->front > 2) return false;
+  if (o->front < 0 || o->front > 3) return false;
   if (o->algo == MOAT_GEMM_DOT2 && n > kMaxDot2N) return false;
   return true;
 }
@@ -101,7 +101,7 @@ GemmPlan plan_gemm(int32_t n, int32_t k, int32_t m, const moat_int4_gemm_options
   const int per_wave = (rounds + 4 * splits - 1) / (4 * splits);
   p.batch = opt.batch ? opt.batch : (per_wave >= 4 ? 4 : (per_wave >= 2 ? 2 : 1));
   p.finish = opt.finish ? opt.finish - 1 : 0;
-  p.staged = opt.front == MOAT_FRONT_DIRECT ? 0 : 1;
+  p.front = opt.front == MOAT_FRONT_DIRECT ? 0 : (opt.front == MOAT_FRONT_LDS_DMA ? 1 : 2);
   if (splits > 1) {
     p.counter_bytes = kCounterBlockBytes;
     p.workspace_bytes = p.counter_bytes + (int64_t)splits * n * m * 4;
@@ -160,7 +160,7 @@ int32_t moat_int4_gemm_ex(const uint16_t* x_f16, const uint8_t* superblocks, flo
     partials = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + p.counter_bytes);
   }
   return status_of(moat::launch_gemm(p.algo, x_f16, superblocks, y_f32, n, k, m, p.splits, p.batch, p.finish,
-                                     p.staged, partials, counters, stream));
+                                     p.front, partials, counters, stream));
 }
 
 int32_t moat_int4_gemm(const uint16_t* x_f16, const uint8_t* superblocks, float* y_f32, int32_t n, int32_t k,

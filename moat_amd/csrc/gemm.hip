@@ -19,12 +19,14 @@
 //    costs one memory latency rather than one latency per round; whole
 //    batches run unconditionally and only the last round of the matrix is
 //    masked;
-//  * weight loads, two front ends:
-//    - LDS-staged (M % 64 == 0): a round's 32 rows x 4 group chunks (2 KB)
-//      and the 4 scales of each row (256 B) are copied HBM -> LDS with three
-//      global_load_lds instructions (dwordx4 / dword per lane); the load slots
-//      are ordered so that lane l's dword of row t lands at byte 256*t + 4*l,
-//      making the read-back one conflict-free 256-byte access per row;
+//  * weight loads, three front ends:
+//    - staged through LDS (M % 64 == 0): a round's 32 rows x 4 group chunks
+//      (2 KB) and the 4 scales of each row (256 B) are fetched as three load
+//      slots per lane (two 16-byte, one 4-byte) and put into a per-wave LDS
+//      stage, either with plain vector loads + ds_write (kFrontVgprLds) or
+//      with global_load_lds (kFrontLdsDma); the slots are ordered so that
+//      lane l's dword of row t sits at byte 256*t + 4*l, making the read-back
+//      one conflict-free 256-byte access per row;
 //    - direct (any M % 32 == 0): 8 dword + 8 scale loads per lane and round
 //      straight into registers;
 //  * the nibbles are turned into (row t, row t+1) fp16 pairs per column
@@ -178,6 +180,33 @@ __device__ __forceinline__ void stage_round(const StageOffsets& o, const uint8_t
   }
   if (o.sc_ok && (!kMasked || round_row0 + o.sc_row < k))
     __builtin_amdgcn_global_load_lds((const void*)(base + o.sc), (lds_ptr_t)(dst + kStagePayload), 4, 0, 0);
+}
+
+// The same three slots loaded into registers (16-byte and 4-byte vector
+// loads) and then written to the stage with ds_write: a plain dwordx4 load
+// moves 1 KB per wave instruction, the widest the vector memory path takes.
+struct SlotRegs {
+  uint4 pay[2];
+  uint32_t sc;
+};
+
+template <bool kMasked>
+__device__ __forceinline__ void slot_load(SlotRegs& v, const StageOffsets& o, const uint8_t* __restrict__ base,
+                                          int round_row0, int k) {
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    if (o.pay_ok[i] && (!kMasked || round_row0 + o.pay_row[i] < k))
+      v.pay[i] = *reinterpret_cast<const uint4*>(base + o.pay[i]);
+    else
+      v.pay[i] = uint4{0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u};
+  }
+  v.sc = (o.sc_ok && (!kMasked || round_row0 + o.sc_row < k)) ? *reinterpret_cast<const uint32_t*>(base + o.sc) : 0u;
+}
+
+__device__ __forceinline__ void slot_store(const SlotRegs& v, uint8_t* dst, int lane) {
+  *reinterpret_cast<uint4*>(dst + 16 * lane) = v.pay[0];
+  *reinterpret_cast<uint4*>(dst + 1024 + 16 * lane) = v.pay[1];
+  *reinterpret_cast<uint32_t*>(dst + kStagePayload + 4 * lane) = v.sc;
 }
 
 // Read one staged round back in the RoundData layout.  Columns outside the
@@ -358,10 +387,17 @@ __device__ __forceinline__ void block_coords(const GemmParams& P, int& tile, int
 
 // ---------------------------------------------------------------------------
 // The kernel: kMfma selects MFMA (NR = 16-row blocks of X) or dot2 (NR = rows
-// of X); kStaged selects the LDS-staged or the direct front end.
+// of X); kFront selects how weights reach the registers.
 
-template <bool kMfma, int NR, int kBatch, bool kStaged>
+enum Front : int {
+  kFrontDirect = 0,   // 4-byte loads straight into the operand layout
+  kFrontLdsDma = 1,   // global_load_lds into the stage, ds_read back
+  kFrontVgprLds = 2,  // dwordx4 loads, ds_write into the stage, ds_read back
+};
+
+template <bool kMfma, int NR, int kBatch, int kFront>
 __global__ void __launch_bounds__(kThreads) int4_gemm_kernel(GemmParams P) {
+  constexpr bool kStaged = kFront != kFrontDirect;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int j = lane & 15, q = lane >> 4, a = j >> 2;
@@ -403,15 +439,21 @@ __global__ void __launch_bounds__(kThreads) int4_gemm_kernel(GemmParams P) {
   for (; r + (kBatch - 1) * kWaves < r_full_end; r += kWaves * kBatch) {
     half8_t xr[kBatch][NR];
     RoundData d[kStaged ? 1 : kBatch];
+    SlotRegs sr[kFront == kFrontVgprLds ? kBatch : 1];
 #pragma unroll
     for (int i = 0; i < kBatch; ++i) {
       const int ri = r + i * kWaves;
       const uint8_t* base = P.sb + ri * round_bytes;
-      if constexpr (kStaged) stage_round<false>(so, base, ri * kRoundRows, P.k, stage + i * kStageRound);
+      if constexpr (kFront == kFrontLdsDma) stage_round<false>(so, base, ri * kRoundRows, P.k, stage + i * kStageRound);
+      else if constexpr (kFront == kFrontVgprLds) slot_load<false>(sr[i], so, base, ri * kRoundRows, P.k);
       else direct_round<false>(d[i], dof, base, smask, ri * kRoundRows + 8 * q, P.k);
       load_x_round<kMfma, NR>(xr[i], P, j, ri * kRoundRows + 8 * q, xfast_ok);
     }
-    if constexpr (kStaged) __builtin_amdgcn_s_waitcnt(0);  // this batch's LDS copies have landed
+    if constexpr (kFront == kFrontLdsDma) __builtin_amdgcn_s_waitcnt(0);  // this batch's LDS copies have landed
+    if constexpr (kFront == kFrontVgprLds) {
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) slot_store(sr[i], stage + i * kStageRound, lane);
+    }
 #pragma unroll
     for (int i = 0; i < kBatch; ++i) {
       if constexpr (kStaged) {
@@ -421,7 +463,7 @@ __global__ void __launch_bounds__(kThreads) int4_gemm_kernel(GemmParams P) {
         compute_round<kMfma, NR>(acc, d[i], xr[i], mw);
       }
     }
-    if constexpr (kStaged) __builtin_amdgcn_s_waitcnt(0);  // reads done before the stage is refilled
+    if constexpr (kFront == kFrontLdsDma) __builtin_amdgcn_s_waitcnt(0);  // reads done before the stage is refilled
   }
   // remaining rounds one at a time; only a round reaching past K is masked
   for (; r < r_end; r += kWaves) {
@@ -432,9 +474,16 @@ __global__ void __launch_bounds__(kThreads) int4_gemm_kernel(GemmParams P) {
     RoundData d;
     load_x_round<kMfma, NR>(xr[0], P, j, row0 + 8 * q, xfast_ok && row0 + 8 * q + 8 <= P.k);
     if constexpr (kStaged) {
-      if (masked) stage_round<true>(so, base, row0, P.k, stage);
-      else stage_round<false>(so, base, row0, P.k, stage);
-      __builtin_amdgcn_s_waitcnt(0);
+      if constexpr (kFront == kFrontLdsDma) {
+        if (masked) stage_round<true>(so, base, row0, P.k, stage);
+        else stage_round<false>(so, base, row0, P.k, stage);
+        __builtin_amdgcn_s_waitcnt(0);
+      } else {
+        SlotRegs v;
+        if (masked) slot_load<true>(v, so, base, row0, P.k);
+        else slot_load<false>(v, so, base, row0, P.k);
+        slot_store(v, stage, lane);
+      }
       if (masked) read_round<true>(d, stage, lane, q, a, sc_sel, row0, P.k, smask);
       else read_round<false>(d, stage, lane, q, a, sc_sel, row0, P.k, smask);
     } else {
@@ -442,7 +491,7 @@ __global__ void __launch_bounds__(kThreads) int4_gemm_kernel(GemmParams P) {
       else direct_round<false>(d, dof, base, smask, row0 + 8 * q, P.k);
     }
     compute_round<kMfma, NR>(acc, d, xr[0], mw);
-    if constexpr (kStaged) __builtin_amdgcn_s_waitcnt(0);
+    if constexpr (kFront == kFrontLdsDma) __builtin_amdgcn_s_waitcnt(0);
   }
   if constexpr (kStaged) __syncthreads();  // the stage area is reused for the tile reduction
 
@@ -513,53 +562,55 @@ int gemm_rounds(int k) { return (k + kRoundRows - 1) / kRoundRows; }
 
 static size_t reduce_lds(int npad) { return (size_t)2 * npad * kTileCols * sizeof(float); }
 
-template <bool kMfma, int NR, int B, bool kStaged>
+template <bool kMfma, int NR, int B, int kFront>
 static void launch_one(const GemmParams& P, hipStream_t stream) {
   const size_t red = reduce_lds(kMfma ? NR * 16 : NR);
-  const size_t stg = kStaged ? (size_t)kWaves * B * kStageRound : 0;
-  hipLaunchKernelGGL((int4_gemm_kernel<kMfma, NR, B, kStaged>), dim3(P.tiles * P.splits), dim3(kThreads),
+  const size_t stg = kFront != kFrontDirect ? (size_t)kWaves * B * kStageRound : 0;
+  hipLaunchKernelGGL((int4_gemm_kernel<kMfma, NR, B, kFront>), dim3(P.tiles * P.splits), dim3(kThreads),
                      red > stg ? red : stg, stream, P);
 }
 
-template <int B, bool kStaged>
+template <int B, int kFront>
 static hipError_t launch_gemm_variant(const GemmParams& P, int algo, hipStream_t stream) {
   if (algo == 2) {
-    if (P.n <= 16) launch_one<true, 1, B, kStaged>(P, stream);
-    else launch_one<true, 2, B, kStaged>(P, stream);
+    if (P.n <= 16) launch_one<true, 1, B, kFront>(P, stream);
+    else launch_one<true, 2, B, kFront>(P, stream);
     return hipGetLastError();
   }
   switch (P.n) {
-    case 1: launch_one<false, 1, B, kStaged>(P, stream); break;
-    case 2: launch_one<false, 2, B, kStaged>(P, stream); break;
-    case 3: launch_one<false, 3, B, kStaged>(P, stream); break;
-    case 4: launch_one<false, 4, B, kStaged>(P, stream); break;
-    case 5: launch_one<false, 5, B, kStaged>(P, stream); break;
-    case 6: launch_one<false, 6, B, kStaged>(P, stream); break;
-    case 7: launch_one<false, 7, B, kStaged>(P, stream); break;
-    case 8: launch_one<false, 8, B, kStaged>(P, stream); break;
+    case 1: launch_one<false, 1, B, kFront>(P, stream); break;
+    case 2: launch_one<false, 2, B, kFront>(P, stream); break;
+    case 3: launch_one<false, 3, B, kFront>(P, stream); break;
+    case 4: launch_one<false, 4, B, kFront>(P, stream); break;
+    case 5: launch_one<false, 5, B, kFront>(P, stream); break;
+    case 6: launch_one<false, 6, B, kFront>(P, stream); break;
+    case 7: launch_one<false, 7, B, kFront>(P, stream); break;
+    case 8: launch_one<false, 8, B, kFront>(P, stream); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }
 
+template <int kFront>
+static hipError_t launch_front(const GemmParams& P, int algo, int batch, hipStream_t stream) {
+  if (batch >= 4) return launch_gemm_variant<4, kFront>(P, algo, stream);
+  if (batch == 2) return launch_gemm_variant<2, kFront>(P, algo, stream);
+  return launch_gemm_variant<1, kFront>(P, algo, stream);
+}
+
 hipError_t launch_gemm(int algo, const uint16_t* x, const uint8_t* sb, float* y, int n, int k, int m, int splits,
-                       int batch, int finish, int staged, float* partials, uint32_t* counters, hipStream_t stream) {
+                       int batch, int finish, int front, float* partials, uint32_t* counters, hipStream_t stream) {
   GemmParams P;
   P.x = x; P.sb = sb; P.y = y; P.partials = partials; P.counters = counters;
   P.n = n; P.k = k; P.m = m; P.splits = splits; P.rounds = gemm_rounds(k); P.tiles = gemm_col_tiles(m);
   P.x_vec = ((reinterpret_cast<uintptr_t>(x) & 15) == 0 && (k % 8) == 0) ? 1 : 0;
   P.finish = finish;
-  const bool st = staged != 0 && (m % 64) == 0;
+  // the staged front ends need M % 64 == 0 (4-byte aligned scale pairs)
+  if ((m % 64) != 0) front = kFrontDirect;
   hipError_t e;
-  if (st) {
-    if (batch >= 4) e = launch_gemm_variant<4, true>(P, algo, stream);
-    else if (batch == 2) e = launch_gemm_variant<2, true>(P, algo, stream);
-    else e = launch_gemm_variant<1, true>(P, algo, stream);
-  } else {
-    if (batch >= 4) e = launch_gemm_variant<4, false>(P, algo, stream);
-    else if (batch == 2) e = launch_gemm_variant<2, false>(P, algo, stream);
-    else e = launch_gemm_variant<1, false>(P, algo, stream);
-  }
+  if (front == kFrontLdsDma) e = launch_front<kFrontLdsDma>(P, algo, batch, stream);
+  else if (front == kFrontVgprLds) e = launch_front<kFrontVgprLds>(P, algo, batch, stream);
+  else e = launch_front<kFrontDirect>(P, algo, batch, stream);
   if (e != hipSuccess || splits == 1 || finish != kFinishSecondKernel) return e;
   const int64_t nm = (int64_t)n * m;
   int64_t blocks = (nm + 255) / 256;

@@ -77,7 +77,7 @@ def test_gemm_rejects_null_and_misaligned(lib):
     # dot2 kernel only up to N = 8; unknown algo / batch / finish values are refused
     for opt in (_lib.GemmOptions(_lib.GEMM_DOT2, 1, 0, 0),):
         assert lib.moat_int4_gemm_ex(FAKE, FAKE, FAKE, 9, 256, 256, ctypes.byref(opt), None, 0, None) == _lib.MOAT_ERR_INVALID
-    for opt in (_lib.GemmOptions(7, 1, 0, 0), _lib.GemmOptions(0, 1, 3, 0), _lib.GemmOptions(0, 1, 0, 4), _lib.GemmOptions(0, 1, 0, 0, 3),
+    for opt in (_lib.GemmOptions(7, 1, 0, 0), _lib.GemmOptions(0, 1, 3, 0), _lib.GemmOptions(0, 1, 0, 4), _lib.GemmOptions(0, 1, 0, 0, 4),
                 _lib.GemmOptions(0, -1, 0, 0)):
         assert lib.moat_int4_gemm_ex(FAKE, FAKE, FAKE, 1, 256, 256, ctypes.byref(opt), None, 0, None) == _lib.MOAT_ERR_INVALID
         assert lib.moat_int4_gemm_ex_workspace_size(1, 256, 256, ctypes.byref(opt)) == -1

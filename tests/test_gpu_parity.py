@@ -140,8 +140,8 @@ def test_gemm_matches_oracle_all_kernels(name, ns):
         xd = torch.from_numpy(x).cuda()
         algos = [L.GEMM_AUTO, L.GEMM_MFMA] + ([L.GEMM_DOT2] if N <= 8 else [])
         for algo in algos:
-            for splits, batch, finish, front in ((0, 0, 0, 0), (1, 0, 0, 1), (1, 0, 0, 2), (3, 1, 1, 1), (3, 2, 2, 2),
-                                                 (7, 4, 3, 1), (5, 4, 1, 2)):
+            for splits, batch, finish, front in ((0, 0, 0, 0), (1, 0, 0, 1), (1, 0, 0, 2), (1, 0, 0, 3), (3, 1, 1, 1),
+                                                 (3, 2, 2, 2), (7, 4, 3, 1), (5, 4, 1, 2), (6, 4, 1, 3), (2, 2, 3, 3)):
                 say(f"case: gemm {name} N={N} algo={algo} splits={splits} batch={batch} finish={finish} front={front}")
                 y = batched_int4_matmul(xd, blob_d, K, M, algo=algo, splits=splits, batch=batch, finish=finish,
                                         front=front)
@@ -195,7 +195,7 @@ def test_gemm_ragged_shapes(K, M):
         for algo in (L.GEMM_MFMA, L.GEMM_DOT2):
             if algo == L.GEMM_DOT2 and N > 8:
                 continue
-            for splits, batch, front in ((1, 1, 1), (2, 2, 1), (2, 4, 1), (1, 1, 2), (2, 4, 2)):
+            for splits, batch, front in ((1, 1, 1), (2, 2, 1), (2, 4, 1), (1, 1, 2), (2, 4, 2), (1, 2, 3), (2, 4, 3)):
                 say(f"case: ragged K={K} M={M} N={N} algo={algo} splits={splits} batch={batch} front={front}")
                 y = batched_int4_matmul(x, blob, K, M, algo=algo, splits=splits, batch=batch, front=front)
                 assert rel_err(y, yref) <= TOL, (K, M, N, algo, splits, batch, front)
