@@ -27,16 +27,16 @@ import numpy as np
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, 8 TB/s
 CONFIGS = {
     # name: (K, M, weight std, weight seed, outlier fraction, default Ns)
-    "cfg1": (2048, 2048, 0.02, 1001, 0.0, [8]),
-    "cfg2": (2048, 5504, 0.02, 1002, 0.0, [1, 2, 4, 8, 16, 32]),
-    "cfg3": (3072, 8192, 0.02, 1003, 0.0, [1, 2, 4, 8, 16, 32]),
-    "cfg5": (8192, 28672, 0.01, 1005, 0.001, [1, 32]),
+    "k2048_m2048": (2048, 2048, 0.02, 1001, 0.0, [8]),
+    "k2048_m5504": (2048, 5504, 0.02, 1002, 0.0, [1, 2, 4, 8, 16, 32]),
+    "k3072_m8192": (3072, 8192, 0.02, 1003, 0.0, [1, 2, 4, 8, 16, 32]),
+    "k8192_m28672": (8192, 28672, 0.01, 1005, 0.001, [1, 32]),
 }
 WORKLOAD_NAMES = {
-    "cfg1": "int4 superblock projection 2048x2048",
-    "cfg2": "int4 superblock FFN gate/up projection K=2048 M=5504, N sweep 1..32",
-    "cfg3": "int4 superblock FFN projection K=3072 M=8192, N sweep 1..32",
-    "cfg5": "int4 superblock projection K=8192 M=28672 (70B-class FFN, 0.1% 8-sigma outliers)",
+    "k2048_m2048": "int4 superblock projection 2048x2048",
+    "k2048_m5504": "int4 superblock FFN gate/up projection K=2048 M=5504, N sweep 1..32",
+    "k3072_m8192": "int4 superblock FFN projection K=3072 M=8192, N sweep 1..32",
+    "k8192_m28672": "int4 superblock projection K=8192 M=28672 (70B-class FFN, 0.1% 8-sigma outliers)",
 }
 ROTATE_BYTES = 300 * 1024 * 1024
 
@@ -94,7 +94,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="cfg2", choices=sorted(CONFIGS))
+    ap.add_argument("--config", default="k2048_m5504", choices=sorted(CONFIGS))
     ap.add_argument("--ns", default=None, help="comma-separated N values (default: the config's)")
     ap.add_argument("--algo", type=int, default=0, help="0 auto, 1 dot2, 2 mfma")
     ap.add_argument("--splits", type=int, default=0)
@@ -103,6 +103,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--batch", type=int, default=0, help="rounds of loads issued together (0 auto)")
     ap.add_argument("--finish", type=int, default=0, help="split-K hand-off (0 auto, 1 atomics, 2 fences, 3 kernel)")
+    ap.add_argument("--front", type=int, default=0, help="load front end (0 auto, 1 LDS-staged, 2 direct, 3 LDS DMA)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -139,7 +140,8 @@ def main() -> int:
     ys = {N: torch.empty((N, M), dtype=torch.float32, device=dev) for N in ns}
 
     def one_call(N, i):
-        _gemm_into(xs[N], blobs[i % copies], ys[N], K, M, args.algo, args.splits, args.batch, args.finish)
+        _gemm_into(xs[N], blobs[i % copies], ys[N], K, M, args.algo, args.splits, args.batch, args.finish,
+                   args.front)
 
     # All timed work is replayed from HIP graphs captured on one stream, so the
     # timed region holds back-to-back kernels and no Python launch overhead.
@@ -237,11 +239,13 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int4-superblock weights, fp16 activations, fp32 accumulate",
+        "dtype": "f16",  # dequantized weights and activations in fp16, products summed in fp32
         "data": "synthetic",
         "config": {"workload": WORKLOAD_NAMES[args.config], "K": K, "M": M, "ns": ns,
                    "weight_copies_rotated": copies, "timing": "HIP graph replay, HIP events on the launch stream",
-                   "algo": args.algo, "splits": args.splits, "batch": args.batch, "finish": args.finish},
+                   "algo": args.algo, "splits": args.splits, "batch": args.batch, "finish": args.finish,
+                   "front": args.front, "weights": "int4 superblocks (144 B per 256 weights)",
+                   "activations": "fp16", "output": "fp32"},
         "per_n": {str(k): v for k, v in per_n.items()},
         "roofline": roof,
         "cpu_baseline": cpu,

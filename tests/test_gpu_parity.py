@@ -81,12 +81,12 @@ def test_dequant_kernel_kat_0x7f():
 
 
 SHAPES = {
-    "cfg1 2048x2048": (2048, 2048, 0.02, 1001, 0.0),
-    "cfg2 2048x5504": (2048, 5504, 0.02, 1002, 0.0),
-    "cfg3 3072x8192": (3072, 8192, 0.02, 1003, 0.0),
-    "cfg4 qkvo 2048x2048": (2048, 2048, 0.02, 1004, 0.0),
-    "cfg4 gate/up 2048x5632": (2048, 5632, 0.02, 1014, 0.0),
-    "cfg4 down 5632x2048": (5632, 2048, 0.02, 1024, 0.0),
+    "proj 2048x2048": (2048, 2048, 0.02, 1001, 0.0),
+    "ffn 2048x5504": (2048, 5504, 0.02, 1002, 0.0),
+    "ffn 3072x8192": (3072, 8192, 0.02, 1003, 0.0),
+    "layer qkvo 2048x2048": (2048, 2048, 0.02, 1004, 0.0),
+    "layer gate/up 2048x5632": (2048, 5632, 0.02, 1014, 0.0),
+    "layer down 5632x2048": (5632, 2048, 0.02, 1024, 0.0),
 }
 
 _cache = {}
@@ -118,12 +118,12 @@ def _x(N, K, seed):
 
 
 GEMM_CASES = [
-    ("cfg1 2048x2048", [8]),
-    ("cfg2 2048x5504", [1, 2, 4, 8, 16, 32]),
-    ("cfg3 3072x8192", [1, 8, 32]),
-    ("cfg4 qkvo 2048x2048", [16]),
-    ("cfg4 gate/up 2048x5632", [16]),
-    ("cfg4 down 5632x2048", [16]),
+    ("proj 2048x2048", [8]),
+    ("ffn 2048x5504", [1, 2, 4, 8, 16, 32]),
+    ("ffn 3072x8192", [1, 8, 32]),
+    ("layer qkvo 2048x2048", [16]),
+    ("layer gate/up 2048x5632", [16]),
+    ("layer down 5632x2048", [16]),
 ]
 
 
@@ -152,7 +152,7 @@ def test_gemm_matches_oracle_all_kernels(name, ns):
 def test_gemm_equals_stacked_gemv():
     """GEMM(N) == N single-row products (antigravity-engine/tests/test_batched_speed.py:55-86)."""
     from moat_amd.dequant import batched_int4_matmul
-    K, M, _, blob = workload("cfg3 3072x8192")
+    K, M, _, blob = workload("ffn 3072x8192")
     blob_d = torch.from_numpy(blob.reshape(-1)).cuda()
     for N in (8, 32):
         x = torch.from_numpy(_x(N, K, 77 + N)).cuda()
@@ -221,7 +221,7 @@ def test_gemm_split_k_handoff_is_deterministic():
     """Every split-K hand-off gives the same bits on every call (partials are
     added in split order), and the hand-offs agree with each other."""
     from moat_amd.dequant import batched_int4_matmul
-    K, M, _, blob = workload("cfg2 2048x5504")
+    K, M, _, blob = workload("ffn 2048x5504")
     blob_d = torch.from_numpy(blob.reshape(-1)).cuda()
     for N in (1, 4, 32):
         x = torch.from_numpy(_x(N, K, 3)).cuda()
@@ -243,7 +243,7 @@ def test_gemm_n_above_32_is_sliced():
     assert rel_err(y, O.gemm_ref(x, blob, K, M)) <= TOL
 
 
-BIG = {"cfg5 8192x28672": (8192, 28672, 0.01, 1005, 0.001)}
+BIG = {"proj 8192x28672": (8192, 28672, 0.01, 1005, 0.001)}
 
 
 def test_large_projection_with_outliers():
@@ -251,7 +251,7 @@ def test_large_projection_with_outliers():
     from moat_amd.dequant import batched_int4_matmul, quantize_to_superblocks
     K, M = 8192, 28672
     w = O.synthetic_weights(K, M, 0.01, 1005, outlier_frac=0.001)
-    say("case: cfg5 quantize on GPU")
+    say("case: 8192x28672 quantize on GPU")
     blob_d = quantize_to_superblocks(torch.from_numpy(w).cuda())
     blob = blob_d.cpu().numpy()
     q, s = O.quantize_a(w.reshape(-1))
@@ -260,7 +260,7 @@ def test_large_projection_with_outliers():
     wdq = O.decode_superblocks(blob, K * M // 256).astype(np.float32).reshape(K, M)
     for N in (1, 32):
         x = _x(N, K, 2500 + N)
-        say(f"case: cfg5 gemm N={N}")
+        say(f"case: 8192x28672 gemm N={N}")
         y = batched_int4_matmul(torch.from_numpy(x).cuda(), blob_d, K, M).cpu().numpy()
         assert rel_err(y, x.astype(np.float32) @ wdq) <= TOL
 
