@@ -96,10 +96,14 @@ int32_t moat_int4_gemm(const uint16_t* x_f16, const uint8_t* superblocks, float*
 /* Launch choices for moat_int4_gemm_ex; zero-initialise for "automatic". */
 typedef struct moat_int4_gemm_options {
   int32_t algo;   /* MOAT_GEMM_*: 0 automatic, 1 dot2 (n <= 8), 2 MFMA */
-  int32_t splits; /* K slices, >= 1; 0 automatic */
-  int32_t batch;  /* 32-row rounds whose loads a wave issues together: 1, 2 or 4; 0 automatic */
+  int32_t splits; /* K slices per column tile, >= 1; 0 automatic (record-stream kernel: workgroups
+                     per tile group, each taking an equal run of (tile group, round) items) */
+  int32_t batch;  /* 32-row rounds a wave has in flight: 1..4 (general kernel: 1, 2 or 4 issued
+                     together; record-stream kernel: ring depth, 3 at most); 0 automatic */
   int32_t finish; /* split-K hand-off, MOAT_FINISH_*; 0 automatic */
   int32_t front;  /* weight loads, MOAT_FRONT_*; 0 automatic */
+  int32_t group;  /* record-stream kernel: adjacent 256-column tiles per workgroup, 1, 2 or 4
+                     (the 4 waves split 4 / group ways over K); 0 automatic */
 } moat_int4_gemm_options;
 
 #define MOAT_FINISH_AUTO 0
@@ -111,6 +115,9 @@ typedef struct moat_int4_gemm_options {
 #define MOAT_FRONT_LDS 1     /* 16-byte vector loads staged through LDS (m % 64 == 0; otherwise direct) */
 #define MOAT_FRONT_DIRECT 2  /* 4-byte loads straight into registers */
 #define MOAT_FRONT_LDS_DMA 3 /* global_load_lds staging (m % 64 == 0; otherwise direct) */
+#define MOAT_FRONT_RECORDS 4 /* record-stream kernel: whole 144-byte records per row, 256-column tiles,
+                                matrix cores (m % 128 == 0, k % 32 == 0, x 16-byte aligned; otherwise
+                                the general kernel) -- the automatic choice when the shape allows it */
 
 /* Same product with the launch choices made by the caller (NULL = all
  * automatic): for measurement and for testing each kernel at every n.

@@ -24,13 +24,14 @@ DTYPE_F32, DTYPE_F16, DTYPE_I8, DTYPE_F64, DTYPE_I64 = 0, 1, 2, 3, 4
 SCALE_F32, SCALE_F16 = 0, 1
 GEMM_AUTO, GEMM_DOT2, GEMM_MFMA = 0, 1, 2
 FINISH_AUTO, FINISH_DEVICE_ATOMICS, FINISH_FENCES, FINISH_SECOND_KERNEL = 0, 1, 2, 3
-FRONT_AUTO, FRONT_LDS, FRONT_DIRECT, FRONT_LDS_DMA = 0, 1, 2, 3
+FRONT_AUTO, FRONT_LDS, FRONT_DIRECT, FRONT_LDS_DMA, FRONT_RECORDS = 0, 1, 2, 3, 4
 
 
 class GemmOptions(ctypes.Structure):
     """``moat_int4_gemm_options``: zero fields mean automatic."""
     _fields_ = [("algo", ctypes.c_int32), ("splits", ctypes.c_int32),
-                ("batch", ctypes.c_int32), ("finish", ctypes.c_int32), ("front", ctypes.c_int32)]
+                ("batch", ctypes.c_int32), ("finish", ctypes.c_int32), ("front", ctypes.c_int32),
+                ("group", ctypes.c_int32)]
 
 _P = ctypes.c_void_p
 _I32 = ctypes.c_int32

@@ -24,8 +24,13 @@ hipError_t launch_pack_superblocks(const int8_t* q, const uint16_t* scales, int6
 hipError_t launch_quantize_pack(const void* w, int dtype, int64_t n, int scale_mode, uint8_t* sb, hipStream_t st);
 int gemm_col_tiles(int m);
 int gemm_rounds(int k);
+bool gemm_records_eligible(int k, int m);
+int gemm_records_tiles(int m);
+int gemm_records_groups(int m, int group_tiles);
+bool gemm_records_shares_tiles(int k, int m, int group_tiles, int wgs);
 hipError_t launch_gemm(int algo, const uint16_t* x, const uint8_t* sb, float* y, int n, int k, int m, int splits,
-                       int batch, int finish, int front, float* partials, uint32_t* counters, hipStream_t stream);
+                       int batch, int finish, int front, int group, float* partials, uint32_t* counters,
+                       hipStream_t stream);
 }  // namespace moat
 
 namespace {
@@ -47,7 +52,8 @@ struct GemmPlan {
   int splits;
   int batch;
   int finish;  // kernel-side FinishMode: 0 device atomics, 1 fences, 2 second kernel
-  int front;   // kernel-side front end: 0 direct, 1 LDS DMA, 2 vector loads + LDS
+  int front;   // kernel-side front end: 0 direct, 1 LDS DMA, 2 vector loads + LDS, 3 record stream
+  int group;   // record stream: 256-column tiles per workgroup
   int64_t counter_bytes;
   int64_t workspace_bytes;
 };
@@ -64,9 +70,10 @@ bool gemm_shape_ok(int32_t n, int32_t k, int32_t m) {
 bool options_ok(const moat_int4_gemm_options* o, int32_t n) {
   if (!o) return true;
   if (o->algo < 0 || o->algo > 2 || o->splits < 0) return false;
-  if (o->batch != 0 && o->batch != 1 && o->batch != 2 && o->batch != 4) return false;
+  if (o->batch < 0 || o->batch > 4) return false;
   if (o->finish < 0 || o->finish > 3) return false;
-  if (o->front < 0 || o->front > 3) return false;
+  if (o->front < 0 || o->front > 4) return false;
+  if (o->group != 0 && o->group != 1 && o->group != 2 && o->group != 4) return false;
   if (o->algo == MOAT_GEMM_DOT2 && n > kMaxDot2N) return false;
   return true;
 }
@@ -77,12 +84,56 @@ bool options_ok(const moat_int4_gemm_options* o, int32_t n) {
 // splits * N * M * 8 bytes against 0.5625 * K * M bytes of weights; it is kept
 // below a quarter of the weight stream.
 GemmPlan plan_gemm(int32_t n, int32_t k, int32_t m, const moat_int4_gemm_options* o) {
-  moat_int4_gemm_options opt = {0, 0, 0, 0, 0};
+  moat_int4_gemm_options opt = {0, 0, 0, 0, 0, 0};
   if (o) opt = *o;
   GemmPlan p;
-  p.algo = opt.algo == MOAT_GEMM_AUTO ? ((n <= 2) ? MOAT_GEMM_DOT2 : MOAT_GEMM_MFMA) : opt.algo;
-  const int tiles = moat::gemm_col_tiles(m);
+  const bool records_ok = moat::gemm_records_eligible(k, m);
+  // the record-stream kernel (matrix cores) serves every N when the shape allows it
+  const bool records = records_ok && opt.algo != MOAT_GEMM_DOT2 &&
+                       (opt.front == MOAT_FRONT_AUTO || opt.front == MOAT_FRONT_RECORDS);
+  if (opt.algo != MOAT_GEMM_AUTO) p.algo = opt.algo;
+  else p.algo = (records || n > 2) ? MOAT_GEMM_MFMA : MOAT_GEMM_DOT2;
   const int rounds = moat::gemm_rounds(k);
+  if (records) {
+    // Record-stream kernel.  Tiles per workgroup: 1 (its 4 waves split K four
+    // ways), measured fastest at every benchmark shape but the largest, where
+    // 2 ties.  Workgroups: a multiple of the tile-group count (so that the
+    // workgroups of neighbouring groups read the same rows at the same time
+    // and share 128-byte lines in L2), about 2 rounds per wave, at most 512
+    // (2 per CU), and a K split whose fp32 partials stay well below the
+    // weight stream.
+    const int group = opt.group ? opt.group : 1;
+    const int groups = moat::gemm_records_groups(m, group);
+    const int64_t tiles_r = moat::gemm_records_tiles(m);
+    int64_t splits;
+    if (opt.splits > 0) {
+      splits = opt.splits;
+    } else {
+      splits = (tiles_r * rounds / 8 + groups / 2) / groups;  // ~2 rounds per wave
+      const int64_t cap_wgs = 512 / groups > 0 ? 512 / groups : 1;
+      if (splits > cap_wgs) splits = cap_wgs;
+      int64_t by_traffic = k / (16 * n);
+      if (by_traffic < 2) by_traffic = 2;
+      if (splits > by_traffic) splits = by_traffic;
+      if (splits < 1) splits = 1;
+    }
+    int64_t wgs = (int64_t)groups * splits;
+    const int64_t items = (int64_t)groups * rounds;
+    if (wgs > items) wgs = items;
+    p.splits = (int)wgs;
+    p.group = group;
+    p.batch = opt.batch ? opt.batch : (n <= 16 ? 3 : 2);  // ring depth (LDS: 4 waves x depth x 6 or 7 KB)
+    p.finish = 2;                          // shared tile groups are summed by the fix-up kernel
+    p.front = 3;
+    // the partials follow the fixed counter block, which other calls sharing
+    // the workspace rely on staying zero
+    const bool shared = moat::gemm_records_shares_tiles(k, m, group, p.splits);
+    p.counter_bytes = shared ? kCounterBlockBytes : 0;
+    p.workspace_bytes =
+        shared ? p.counter_bytes + (int64_t)2 * p.splits * group * n * 256 * (int64_t)sizeof(float) : 0;
+    return p;
+  }
+  const int tiles = moat::gemm_col_tiles(m);
   int splits = opt.splits;
   if (splits <= 0) {
     const int target_wgs = 640;
@@ -97,11 +148,13 @@ GemmPlan plan_gemm(int32_t n, int32_t k, int32_t m, const moat_int4_gemm_options
   }
   if (splits > rounds) splits = rounds;
   p.splits = splits;
-  // rounds per wave in this plan; a wave issues up to 4 rounds of loads at once
-  const int per_wave = (rounds + 4 * splits - 1) / (4 * splits);
+  const int per_wave = (rounds + 4 * splits - 1) / (4 * splits);  // rounds per wave
+  // rounds whose loads a wave issues at once
   p.batch = opt.batch ? opt.batch : (per_wave >= 4 ? 4 : (per_wave >= 2 ? 2 : 1));
-  p.finish = opt.finish ? opt.finish - 1 : 0;
+  // automatic hand-off: a second kernel sums the partials (measured cheapest at every N)
+  p.finish = opt.finish ? opt.finish - 1 : 2;
   p.front = opt.front == MOAT_FRONT_DIRECT ? 0 : (opt.front == MOAT_FRONT_LDS_DMA ? 1 : 2);
+  p.group = 1;
   if (splits > 1) {
     p.counter_bytes = kCounterBlockBytes;
     p.workspace_bytes = p.counter_bytes + (int64_t)splits * n * m * 4;
@@ -154,13 +207,13 @@ int32_t moat_int4_gemm_ex(const uint16_t* x_f16, const uint8_t* superblocks, flo
   if (p.algo == MOAT_GEMM_DOT2 && n > kMaxDot2N) return MOAT_ERR_INVALID;
   float* partials = nullptr;
   uint32_t* counters = nullptr;
-  if (p.splits > 1) {
+  if (p.workspace_bytes > 0) {
     if (!workspace || workspace_bytes < p.workspace_bytes || !aligned(workspace, 16)) return MOAT_ERR_WORKSPACE;
     counters = static_cast<uint32_t*>(workspace);
     partials = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + p.counter_bytes);
   }
   return status_of(moat::launch_gemm(p.algo, x_f16, superblocks, y_f32, n, k, m, p.splits, p.batch, p.finish,
-                                     p.front, partials, counters, stream));
+                                     p.front, p.group, partials, counters, stream));
 }
 
 int32_t moat_int4_gemm(const uint16_t* x_f16, const uint8_t* superblocks, float* y_f32, int32_t n, int32_t k,

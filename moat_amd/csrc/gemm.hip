@@ -76,10 +76,22 @@ struct GemmParams {
   int n, k, m;
   int splits;
   int rounds;              // ceil(k / 32)
-  int tiles;               // ceil(m / 128)
+  int tiles;               // column tiles of the launched kernel: ceil(m / 128), or ceil(m / 256) for records
   int x_vec;               // x is 16-byte aligned and k % 8 == 0: 16-byte X loads
   int finish;              // FinishMode
+  int shift;               // records kernel: M % 256 == 128, odd rows start half-way into a record
+  int rounds_base;         // rounds / splits: split s covers rounds [s*base + min(s, rem), +base + (s < rem))
+  int rounds_rem;          // rounds % splits
+  int y_vec;               // y and the partials are 16-byte aligned and m % 4 == 0: float4 stores
+  int items_base;          // records kernel (stream-K): workgroup p covers items (tile * rounds + round)
+  int items_rem;           //   [p*base + min(p, rem), +base + (p < rem))
 };
+
+// Round range of split s (no device-side division).
+__device__ __forceinline__ void split_rounds(const GemmParams& P, int split, int& r_begin, int& r_end) {
+  r_begin = split * P.rounds_base + min(split, P.rounds_rem);
+  r_end = r_begin + P.rounds_base + (split < P.rounds_rem ? 1 : 0);
+}
 
 // One 32-row round in registers: the lane's payload dword of rows 8q+t and
 // the fp16 scales of rows (8q+2p, 8q+2p+1) packed lo/hi.
@@ -323,12 +335,14 @@ __device__ __forceinline__ float load_partial(const float* p, int finish) {
   return *p;
 }
 
-// Sum the two LDS slots, then store to Y (one split) or publish the partial;
-// the last workgroup of the tile to publish adds all partials in split order.
+// Sum the two LDS slots (each [npad][kCols] floats), then store to Y (one
+// split) or publish the partial; the last workgroup of the tile to publish
+// adds all partials in split order.
+template <int kCols = kTileCols>
 __device__ __forceinline__ void finish_tile(const GemmParams& P, float* red, int npad, int tile, int split) {
   const int tid = threadIdx.x;
-  const int ncols = kTileCols;
-  const int m0 = tile * kTileCols;
+  const int ncols = kCols;
+  const int m0 = tile * kCols;
   const int per_wave = npad * ncols;
   if (P.splits == 1) {
     for (int idx = tid; idx < P.n * ncols; idx += kThreads) {
@@ -376,7 +390,7 @@ __device__ __forceinline__ void finish_tile(const GemmParams& P, float* red, int
 // contiguous logical ranges to each XCD; the logical index is split-major,
 // keeping neighbouring tiles of one K slice together.
 __device__ __forceinline__ void block_coords(const GemmParams& P, int& tile, int& split) {
-  const int total = P.tiles * P.splits;
+  const int total = P.tiles * P.splits;  // P.tiles: column tiles of the launched kernel
   const int b = blockIdx.x;
   const int per = total / kXcds;
   int logical = b;
@@ -393,6 +407,7 @@ enum Front : int {
   kFrontDirect = 0,   // 4-byte loads straight into the operand layout
   kFrontLdsDma = 1,   // global_load_lds into the stage, ds_read back
   kFrontVgprLds = 2,  // dwordx4 loads, ds_write into the stage, ds_read back
+  kFrontRecords = 3,  // the record-stream kernel (int4_gemm_records_kernel)
 };
 
 template <bool kMfma, int NR, int kBatch, int kFront>
@@ -407,8 +422,8 @@ __global__ void __launch_bounds__(kThreads) int4_gemm_kernel(GemmParams P) {
   const bool col_ok = mcol < P.m;
   const uint32_t smask = col_ok ? 0xFFFFFFFFu : 0u;
   const uint64_t round_bytes = (uint64_t)18 * (uint64_t)P.m;  // 32 rows of 0.5625 B per element
-  const int r_begin = (int)((int64_t)split * P.rounds / P.splits);
-  const int r_end = (int)((int64_t)(split + 1) * P.rounds / P.splits);
+  int r_begin, r_end;
+  split_rounds(P, split, r_begin, r_end);
   const bool xfast_ok = P.x_vec != 0;
   const MagicWords mw = magic_words();
 
@@ -543,13 +558,403 @@ __global__ void __launch_bounds__(kThreads) int4_gemm_kernel(GemmParams P) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Record-stream kernel: M % 128 == 0, K % 32 == 0, X rows 16-byte aligned.
+//
+// A workgroup (4 waves) owns a 256-column tile and a K slice; wave w takes
+// rounds w, w+4, ... of the slice.  In every row the tile's bytes are whole
+// 16-byte chunks of at most two records:
+//  * a row that starts on a record boundary (every row when M % 256 == 0,
+//    the even rows when M % 256 == 128) needs the record's header and its 8
+//    payload chunks;
+//  * a row that starts half-way into record s needs the header of s (the
+//    tile's groups 0-3 have their scales at bytes 8..15), payload chunks 4-7
+//    of s, the header of s+1 (groups 4-7 at bytes 0..7) and payload chunks
+//    0-3 of s+1, the last nine being one contiguous 144-byte window.
+// A round (32 rows) is therefore 32 x 10 chunk slots (5 KB), plus the
+// round's X slice (16 rows x 32 fp16 per 16-row block of X).  Both are moved
+// with global_load_lds (16 bytes per lane, straight into LDS) into a
+// per-wave ring of kDepth stages: the wave keeps kDepth - 1 rounds in flight
+// while it computes one, and waits for a round with an explicit vmcnt.
+// Whole records per row touch the fewest 128-byte lines per instruction of
+// any layout of this stream.
+constexpr int kRecCols = 256;
+constexpr int kRecSlotsPerRow = 10;
+constexpr int kRecRowBytes = 16 * kRecSlotsPerRow;          // 160
+constexpr int kRecWeightBytes = kRoundRows * kRecRowBytes;  // 5120: 5 loads of 64 x 16 bytes
+constexpr int kRecWeightLoads = kRecWeightBytes / 1024;
+
+template <int NR>
+struct RecGeom {
+  static constexpr int kStageBytes = kRecWeightBytes + NR * 1024;  // + X: NR loads of 64 x 16 bytes
+  static constexpr int kLoads = kRecWeightLoads + NR;               // vector-memory instructions per round
+};
+
+// Source offsets (round 0) of a lane's weight slots.  Slot s = 64*i + lane
+// carries chunk c = s % 10 of row s / 10 and lands at byte 16*s of the stage,
+// so row t starts at byte 160*t.  Slots that carry nothing the tile needs
+// (chunk 9 of an aligned row, groups past M in the last tile) re-load the
+// row's first header chunk: every round issues the same instructions, which
+// keeps the vmcnt arithmetic exact, and every address stays inside the stream.
+struct RecSlots {
+  uint32_t off[kRecWeightLoads];
+};
+
+__device__ __forceinline__ void rec_slots(RecSlots& s, int lane, int tile, int m, int groups) {
+#pragma unroll
+  for (int i = 0; i < kRecWeightLoads; ++i) {
+    const int slot = 64 * i + lane;
+    const int row = slot / kRecSlotsPerRow, c = slot % kRecSlotsPerRow;
+    const uint32_t flat = (uint32_t)row * (uint32_t)m + (uint32_t)(kRecCols * tile);
+    const uint32_t head = (flat >> 8) * kSbBytes;
+    // record-aligned row: header, then payload chunk c-1 at 16*c
+    const uint32_t al = (c >= 1 && c <= 8 && c - 1 < groups) ? head + 16 * c : head;
+    // shifted row: header of s, chunks 4-7 of s, header of s+1, chunks 0-3 of s+1
+    const bool pay_sh = (c >= 1 && c <= 4) ? (c - 1 < groups) : (c >= 6 && c - 2 < groups);
+    const uint32_t sh = pay_sh ? head + 64 + 16 * c : ((c == 5 && groups > 4) ? head + kSbBytes : head);
+    s.off[i] = ((flat >> 7) & 1) ? sh : al;
+  }
+}
+
+// s_waitcnt vmcnt(N) (gfx9 encoding; expcnt and lgkmcnt left unconstrained),
+// then a compiler barrier so that no LDS read of the stage moves above it.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+  asm volatile("" ::: "memory");
+}
+
+// One global_load_lds_dwordx4: lane l's 16 bytes at `src` land at LDS byte
+// lds_base + 16*l.  Written as inline assembly so that the compiler, which
+// cannot tell the ring's stages apart, does not guard every later LDS read
+// with a wait for all of these copies; the explicit vmcnt waits above are the
+// only ordering the ring needs.  (s_nop: one wait state between writing M0
+// and the instruction that reads it.)
+__device__ __forceinline__ void lds_dma16(const void* src, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(src), "s"(lds_base)
+               : "memory", "m0");
+}
+
+template <int NR>
+__device__ __forceinline__ void rec_issue(const RecSlots& s, const uint8_t* __restrict__ wround,
+                                          const uint8_t* __restrict__ xround, const uint32_t (&xoff)[NR],
+                                          uint32_t stage) {
+#pragma unroll
+  for (int i = 0; i < kRecWeightLoads; ++i) lds_dma16(wround + s.off[i], stage + 1024 * i);
+#pragma unroll
+  for (int nt = 0; nt < NR; ++nt) lds_dma16(xround + xoff[nt], stage + kRecWeightBytes + 1024 * nt);
+}
+
+// Per-lane LDS read offsets inside a stage: payload (8 bytes = the lane's 16
+// columns) and fp16 scale of a row, for rows that start on a record boundary
+// ([0]) and rows that start half-way into one ([1]).
+struct RecReads {
+  uint32_t pay[2];
+  uint32_t sc[2];
+  uint32_t x;
+};
+
+// Accumulators of one wave: 16 MFMA column blocks (block c = columns 16j + c
+// for lane column j) per 16-row block of X.
+template <int NR>
+struct RecAcc {
+  float4_t c[NR][16];
+};
+
+template <int NR>
+__device__ __forceinline__ void rec_compute(RecAcc<NR>& acc, const uint8_t* st, const RecReads& rd, int q,
+                                            uint32_t smask, MagicWords mw) {
+  half8_t xr[NR];
+#pragma unroll
+  for (int nt = 0; nt < NR; ++nt)
+    xr[nt] = *reinterpret_cast<const half8_t*>(st + kRecWeightBytes + 1024 * nt + rd.x);
+  const uint8_t* rows = st + kRecRowBytes * 8 * q;  // rows 8q .. 8q+7 of the round
+  uint2 w[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) w[u] = *reinterpret_cast<const uint2*>(rows + kRecRowBytes * u + rd.pay[u & 1]);
+  uint32_t sp[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const uint32_t lo = *reinterpret_cast<const uint16_t*>(rows + kRecRowBytes * (2 * p) + rd.sc[0]);
+    const uint32_t hi = *reinterpret_cast<const uint16_t*>(rows + kRecRowBytes * (2 * p + 1) + rd.sc[1]);
+    sp[p] = (lo | (hi << 16)) & smask;
+  }
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    half2_t pr[4][8];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const uint32_t a = h ? w[2 * p].y : w[2 * p].x;
+      const uint32_t b = h ? w[2 * p + 1].y : w[2 * p + 1].x;
+      dequant_row_pair(a, b, bitcast<half2_t>(sp[p]), pr[p], mw);
+    }
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      half8_t b;
+      b[0] = pr[0][c][0]; b[1] = pr[0][c][1];
+      b[2] = pr[1][c][0]; b[3] = pr[1][c][1];
+      b[4] = pr[2][c][0]; b[5] = pr[2][c][1];
+      b[6] = pr[3][c][0]; b[7] = pr[3][c][1];
+#pragma unroll
+      for (int nt = 0; nt < NR; ++nt)
+        acc.c[nt][8 * h + c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xr[nt], b, acc.c[nt][8 * h + c], 0, 0, 0);
+    }
+  }
+}
+
+// Work split.  A workgroup covers kC adjacent 256-column tiles (a "tile
+// group"): wave w works on tile w % kC of the group and takes every
+// (4 / kC)-th round, so the waves of one tile share its K range and meet in
+// an LDS reduction, and each row the workgroup reads is kC whole records
+// long (wider runs of a row per CU use the 128-byte lines better).  The items
+// are (tile group, round) pairs in group-major order; workgroup p takes a
+// contiguous range (stream-K), and runs it as segments, one per tile group
+// it touches.  A segment covering a whole group writes Y; any other segment
+// writes fp32 partials into slots 2p (the workgroup's first segment) or
+// 2p + 1 (its last), and the fix-up kernel adds the partials of each shared
+// group in workgroup order, so results are deterministic.
+__device__ __forceinline__ void streamk_range(const GemmParams& P, int p, int& lo, int& hi) {
+  lo = p * P.items_base + min(p, P.items_rem);
+  hi = lo + P.items_base + (p < P.items_rem ? 1 : 0);
+}
+
+// Workgroup whose range holds item i.
+__device__ __forceinline__ int streamk_owner(const GemmParams& P, int i) {
+  const int big = P.items_rem * (P.items_base + 1);
+  return i < big ? i / (P.items_base + 1) : P.items_rem + (i - big) / P.items_base;
+}
+
+// LDS position (floats) of D[row][col] of one tile inside a reduction slot:
+// four consecutive columns form one 16-byte quad, and the quads of column
+// group jj = col / 16 are rotated by jj / 4, so that any 8 consecutive lanes
+// of a row address 8 different 16-byte bank groups.
+__device__ __forceinline__ int red_pos(int row, int jj, int u) {
+  return row * kRecCols + 16 * jj + 4 * ((u + (jj >> 2)) & 3);
+}
+
+// Output of a tile group: tile tl of the group sums `nslots` LDS slots
+// (slot s of tile tl at red + (tl * nslots + s) * per_slot) and goes to Y
+// (part == nullptr) or to the partial slot part + tl * per_slot.  The whole
+// workgroup stores, one 4-column quad per thread and step.
+template <int kC>
+__device__ __forceinline__ void rec_store(const GemmParams& P, const float* red, int per_slot, int nslots, int tg,
+                                          float* part) {
+  const int total = kC * P.n * 64;
+  for (int idx = threadIdx.x; idx < total; idx += kThreads) {
+    const int tl = idx / (P.n * 64);
+    const int w = idx - tl * P.n * 64;
+    const int row = w >> 6, qd = w & 63;
+    const int tile = tg * kC + tl;
+    const int m0 = tile * kRecCols;
+    if (m0 + 4 * qd >= P.m) continue;
+    const float* base = red + tl * nslots * per_slot + red_pos(row, qd >> 2, qd & 3);
+    float4_t v = *reinterpret_cast<const float4_t*>(base);
+    if (nslots > 1) v += *reinterpret_cast<const float4_t*>(base + per_slot);
+    if (part) {
+      *reinterpret_cast<float4_t*>(part + tl * per_slot + row * kRecCols + 4 * qd) = v;
+    } else {
+      float* yp = P.y + (int64_t)row * P.m + m0 + 4 * qd;
+      if (P.y_vec) {
+        *reinterpret_cast<float4_t*>(yp) = v;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) yp[e] = v[e];
+      }
+    }
+  }
+}
+
+template <int NR, int kDepth, int kC>
+__global__ void __launch_bounds__(kThreads) int4_gemm_records_kernel(GemmParams P) {
+  using G = RecGeom<NR>;
+  constexpr int kShare = kWaves / kC;  // waves per tile
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  // fetch every argument now, in one batch of scalar loads, rather than at
+  // first use (each late load is another serial trip to memory)
+  asm volatile("" : : "s"(P.x), "s"(P.sb), "s"(P.y), "s"(P.partials), "s"(P.n), "s"(P.k), "s"(P.m),
+               "s"(P.rounds), "s"(P.shift), "s"(P.y_vec), "s"(P.items_base), "s"(P.items_rem), "s"(P.tiles));
+  const int lane = threadIdx.x & 63;
+  // wave index as a scalar: the round loop below is then uniform control flow
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int tl = wave % kC, kpart = wave / kC;
+  const int j = lane & 15, q = lane >> 4;
+  const int g = j >> 1;  // lane j owns columns 16j .. 16j+15 of a tile (group j/2)
+  const MagicWords mw = magic_words();
+  RecReads rd;
+  rd.pay[0] = 16 + 16 * g + 8 * (j & 1);
+  rd.sc[0] = 2 * g;
+  if (P.shift) {
+    rd.pay[1] = (g >= 4 ? 32 : 16) + 16 * g + 8 * (j & 1);
+    rd.sc[1] = (g < 4 ? 8 : 72) + 2 * g;
+  } else {
+    rd.pay[1] = rd.pay[0];
+    rd.sc[1] = rd.sc[0];
+  }
+  rd.x = 64 * j + 16 * (q ^ (j & 3));
+  // X slice loads: lane l fetches row 16*nt + l/4 (rows past N repeat row N-1;
+  // their products land in output rows that are never stored), 8 fp16 at
+  // column 8 * ((l & 3) ^ ((l >> 2) & 3)) of the round
+  uint32_t xoff[NR];
+#pragma unroll
+  for (int nt = 0; nt < NR; ++nt) {
+    const int row = min(16 * nt + (lane >> 2), P.n - 1);
+    const int chunk = (lane & 3) ^ ((lane >> 2) & 3);
+    xoff[nt] = (uint32_t)(2 * (row * P.k + 8 * chunk));
+  }
+  // workgroup ids are dealt round-robin to the 8 XCDs: give each XCD one
+  // contiguous run of ranges, so that the tiles it shares meet in its L2
+  const int nwg = gridDim.x, b = blockIdx.x, per = nwg / kXcds;
+  const int p = b < per * kXcds ? (b % kXcds) * per + b / kXcds : b;
+  int lo, hi;
+  streamk_range(P, p, lo, hi);
+
+  const uint64_t round_bytes = (uint64_t)18 * (uint64_t)P.m;
+  uint8_t* ring = smem + wave * kDepth * G::kStageBytes;
+  const uint32_t ring_lds = (uint32_t)(uintptr_t)(lds_ptr_t)ring;  // LDS byte address (wave-uniform)
+  float* red = reinterpret_cast<float*>(smem);
+  const int per_slot = P.n * kRecCols;
+  constexpr int kSlots = kShare == 4 ? 2 : 1;  // reduction slots per tile
+
+  for (int seg_lo = lo; seg_lo < hi;) {
+    const int tg = seg_lo / P.rounds;
+    const int r0 = seg_lo - tg * P.rounds;
+    const int seg_hi = min(hi, (tg + 1) * P.rounds);
+    const int r1 = seg_hi - tg * P.rounds;
+    const int tile = tg * kC + tl;
+    const bool has_tile = tile < P.tiles;  // the last group may be short
+    const int groups = has_tile ? min(8, (P.m - kRecCols * tile) >> 5) : 0;  // 4 or 8 (M % 128 == 0)
+    const uint32_t smask = g < groups ? 0xFFFFFFFFu : 0u;
+    RecSlots slots;
+    rec_slots(slots, lane, has_tile ? tile : 0, P.m, has_tile ? groups : 8);
+
+    RecAcc<NR> acc;
+#pragma unroll
+    for (int nt = 0; nt < NR; ++nt)
+#pragma unroll
+      for (int c = 0; c < 16; ++c) acc.c[nt][c] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+    const int first = r0 + kpart;
+    const int cnt = (has_tile && first < r1) ? (r1 - first + kShare - 1) / kShare : 0;
+    auto issue = [&](int i) {
+      const int r = first + kShare * i;
+      rec_issue<NR>(slots, P.sb + (uint64_t)r * round_bytes, reinterpret_cast<const uint8_t*>(P.x) + 64 * r, xoff,
+                    __builtin_amdgcn_readfirstlane(ring_lds + (i % kDepth) * G::kStageBytes));
+    };
+#pragma unroll
+    for (int i = 0; i < kDepth - 1; ++i)
+      if (i < cnt) issue(i);
+    for (int i = 0; i < cnt; ++i) {
+      if (i + kDepth - 1 < cnt) {
+        issue(i + kDepth - 1);
+        wait_vmcnt<(kDepth - 1) * G::kLoads>();
+      } else {
+        const int after = cnt - 1 - i;  // rounds issued after round i: 0 .. kDepth - 2
+        if (kDepth >= 3 && after == 2) wait_vmcnt<(kDepth >= 3 ? 2 * G::kLoads : 0)>();
+        else if (kDepth >= 2 && after == 1) wait_vmcnt<(kDepth >= 2 ? G::kLoads : 0)>();
+        else wait_vmcnt<0>();
+      }
+      rec_compute<NR>(acc, ring + (i % kDepth) * G::kStageBytes, rd, q, smask, mw);
+    }
+    __syncthreads();  // the ring is reused for the reduction
+
+    // Waves of one tile add up through LDS: with 4 waves per tile, waves
+    // with kpart 2, 3 store into the tile's two slots and kpart 0, 1 add
+    // theirs; with 2, kpart 1 stores and kpart 0 adds; with 1 the wave stores.
+    // Lane (q, j) holds D[16*nt + 4q + v][16j + c]; 4 columns per access.
+    float* tred = red + tl * kSlots * per_slot;
+    constexpr int kPhases = kShare > 1 ? 2 : 1;
+#pragma unroll
+    for (int phase = 0; phase < kPhases; ++phase) {
+      const bool active = kShare == 1 ? true : (kShare == 2 ? (kpart == 1 - phase) : ((kpart >> 1) == 1 - phase));
+      const bool add = kShare > 1 && phase == 1;
+      if (active) {
+        float* slot = tred + (kShare == 4 ? (kpart & 1) : 0) * per_slot;
+#pragma unroll
+        for (int nt = 0; nt < NR; ++nt)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int row = nt * 16 + 4 * q + v;
+            if (row < P.n) {
+#pragma unroll
+              for (int u = 0; u < 4; ++u) {
+                float4_t* pp = reinterpret_cast<float4_t*>(slot + red_pos(row, j, u));
+                float4_t val = {acc.c[nt][4 * u][v], acc.c[nt][4 * u + 1][v], acc.c[nt][4 * u + 2][v],
+                                acc.c[nt][4 * u + 3][v]};
+                if (add) val += *pp;
+                *pp = val;
+              }
+            }
+          }
+      }
+      __syncthreads();
+    }
+    const bool whole = r0 == 0 && r1 == P.rounds;
+    const int pslot = 2 * p + (seg_lo == lo ? 0 : 1);
+    rec_store<kC>(P, red, per_slot, kSlots, tg,
+                  whole ? nullptr : P.partials + (int64_t)pslot * kC * per_slot);
+    __syncthreads();  // LDS is the next segment's ring
+    seg_lo = seg_hi;
+  }
+}
+
+// Fix-up of the tile groups that several workgroups share: Y = sum of their
+// partials in workgroup order.  One thread per 4-column quad of a tile.
+__global__ void __launch_bounds__(256) streamk_fixup_kernel(GemmParams P, int group_tiles) {
+  const int per_tile = P.n * 64;
+  const int total = P.tiles * per_tile;
+  const int per_slot = P.n * kRecCols;
+  for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < total; e += gridDim.x * blockDim.x) {
+    const int tile = e / per_tile, w = e - tile * per_tile;
+    const int row = w >> 6, qd = w & 63;
+    const int m0 = tile * kRecCols;
+    if (m0 + 4 * qd >= P.m) continue;
+    const int tg = tile / group_tiles, tl = tile - tg * group_tiles;
+    const int item0 = tg * P.rounds;
+    const int p0 = streamk_owner(P, item0), p1 = streamk_owner(P, item0 + P.rounds - 1);
+    if (p0 == p1) continue;  // one workgroup covered the group and wrote Y
+    // the partials are independent loads: issue 8 before adding any (a
+    // load-then-add loop would pay one memory round trip per partial)
+    float4_t v = {0.f, 0.f, 0.f, 0.f};
+    const int64_t off = (int64_t)tl * per_slot + row * kRecCols + 4 * qd;
+    for (int p8 = p0; p8 <= p1; p8 += 8) {
+      float4_t t[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int pp = min(p8 + i, p1);  // past the end: re-read the last one, added as 0 below
+        const int lo_p = pp * P.items_base + min(pp, P.items_rem);
+        const int pslot = 2 * pp + (lo_p < item0 ? 1 : 0);
+        t[i] = *reinterpret_cast<const float4_t*>(P.partials + (int64_t)pslot * group_tiles * per_slot + off);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i)  // in workgroup order
+        if (p8 + i <= p1) v += t[i];
+    }
+    float* yp = P.y + (int64_t)row * P.m + m0 + 4 * qd;
+    if (P.y_vec) {
+      *reinterpret_cast<float4_t*>(yp) = v;
+    } else {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) yp[k] = v[k];
+    }
+  }
+}
+
 // Second kernel of kFinishSecondKernel: y = sum over splits of the partials.
 __global__ void __launch_bounds__(256) splitk_sum_kernel(const float* __restrict__ partials, int splits,
                                                          int64_t nm, float* __restrict__ y) {
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nm; i += stride) {
+    // 8 independent loads in flight before any add, summed in split order
     float v = 0.0f;
-    for (int s = 0; s < splits; ++s) v += partials[(int64_t)s * nm + i];
+    for (int s8 = 0; s8 < splits; s8 += 8) {
+      float t[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) t[k] = partials[(int64_t)min(s8 + k, splits - 1) * nm + i];
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        if (s8 + k < splits) v += t[k];
+    }
     y[i] = v;
   }
 }
@@ -598,16 +1003,82 @@ static hipError_t launch_front(const GemmParams& P, int algo, int batch, hipStre
   return launch_gemm_variant<1, kFront>(P, algo, stream);
 }
 
+template <int NR, int kDepth, int kC>
+static hipError_t launch_records_one(const GemmParams& P, int wgs, hipStream_t stream) {
+  constexpr int kShare = kWaves / kC;
+  const size_t ring = (size_t)kWaves * kDepth * RecGeom<NR>::kStageBytes;
+  const size_t red = (size_t)kC * (kShare == 4 ? 2 : 1) * P.n * kRecCols * sizeof(float);
+  hipLaunchKernelGGL((int4_gemm_records_kernel<NR, kDepth, kC>), dim3(wgs), dim3(kThreads), ring > red ? ring : red,
+                     stream, P);
+  return hipGetLastError();
+}
+
+template <int NR, int kC>
+static hipError_t launch_records_depth(const GemmParams& P, int wgs, int depth, hipStream_t stream) {
+  if (depth >= 3) return launch_records_one<NR, 3, kC>(P, wgs, stream);
+  if (depth == 2) return launch_records_one<NR, 2, kC>(P, wgs, stream);
+  return launch_records_one<NR, 1, kC>(P, wgs, stream);
+}
+
+template <int NR>
+static hipError_t launch_records(const GemmParams& P, int wgs, int depth, int group_tiles, hipStream_t stream) {
+  if (group_tiles == 4) return launch_records_depth<NR, 4>(P, wgs, depth, stream);
+  if (group_tiles == 2) return launch_records_depth<NR, 2>(P, wgs, depth, stream);
+  return launch_records_depth<NR, 1>(P, wgs, depth, stream);
+}
+
+bool gemm_records_eligible(int k, int m) { return (m % 128) == 0 && (k % kRoundRows) == 0; }
+int gemm_records_tiles(int m) { return (m + kRecCols - 1) / kRecCols; }
+int gemm_records_groups(int m, int group_tiles) { return (gemm_records_tiles(m) + group_tiles - 1) / group_tiles; }
+
+// Workgroups of a stream-K launch share tile groups unless every range is a
+// whole number of groups.
+bool gemm_records_shares_tiles(int k, int m, int group_tiles, int wgs) {
+  const int64_t rounds = k / kRoundRows;
+  const int64_t items = (int64_t)gemm_records_groups(m, group_tiles) * rounds;
+  const int64_t base = items / wgs, rem = items % wgs;
+  return !(rem == 0 && base % rounds == 0);
+}
+
 hipError_t launch_gemm(int algo, const uint16_t* x, const uint8_t* sb, float* y, int n, int k, int m, int splits,
-                       int batch, int finish, int front, float* partials, uint32_t* counters, hipStream_t stream) {
+                       int batch, int finish, int front, int group, float* partials, uint32_t* counters,
+                       hipStream_t stream) {
   GemmParams P;
   P.x = x; P.sb = sb; P.y = y; P.partials = partials; P.counters = counters;
   P.n = n; P.k = k; P.m = m; P.splits = splits; P.rounds = gemm_rounds(k); P.tiles = gemm_col_tiles(m);
   P.x_vec = ((reinterpret_cast<uintptr_t>(x) & 15) == 0 && (k % 8) == 0) ? 1 : 0;
   P.finish = finish;
+  P.shift = 0;
+  P.rounds_base = P.rounds / splits;
+  P.rounds_rem = P.rounds % splits;
+  P.y_vec = ((reinterpret_cast<uintptr_t>(y) & 15) == 0 && (reinterpret_cast<uintptr_t>(partials) & 15) == 0 &&
+             (m % 4) == 0) ? 1 : 0;
+  hipError_t e;
+  if (front == kFrontRecords) {
+    // matrix cores only, whole 32-row rounds, 128-column halves of records and
+    // 16-byte X rows; anything else takes the general kernel's staged front end
+    if (algo == 2 && gemm_records_eligible(k, m) && P.x_vec) {
+      // `splits` is the stream-K workgroup count here
+      const int wgs = splits, group_tiles = group;
+      P.tiles = gemm_records_tiles(m);
+      P.shift = (m % kRecCols) != 0;
+      const int items = gemm_records_groups(m, group_tiles) * P.rounds;
+      P.items_base = items / wgs;
+      P.items_rem = items % wgs;
+      P.y_vec = ((reinterpret_cast<uintptr_t>(y) & 15) == 0) ? 1 : 0;
+      e = P.n <= 16 ? launch_records<1>(P, wgs, batch, group_tiles, stream)
+                    : launch_records<2>(P, wgs, batch, group_tiles, stream);
+      if (e != hipSuccess || !gemm_records_shares_tiles(k, m, group_tiles, wgs)) return e;
+      const int quads = P.tiles * P.n * 64;
+      int blocks = (quads + 255) / 256;
+      if (blocks > 2048) blocks = 2048;
+      hipLaunchKernelGGL(streamk_fixup_kernel, dim3(blocks), dim3(256), 0, stream, P, group_tiles);
+      return hipGetLastError();
+    }
+    front = kFrontVgprLds;
+  }
   // the staged front ends need M % 64 == 0 (4-byte aligned scale pairs)
   if ((m % 64) != 0) front = kFrontDirect;
-  hipError_t e;
   if (front == kFrontLdsDma) e = launch_front<kFrontLdsDma>(P, algo, batch, stream);
   else if (front == kFrontVgprLds) e = launch_front<kFrontVgprLds>(P, algo, batch, stream);
   else e = launch_front<kFrontDirect>(P, algo, batch, stream);

@@ -77,22 +77,36 @@ def test_gemm_rejects_null_and_misaligned(lib):
     # dot2 kernel only up to N = 8; unknown algo / batch / finish values are refused
     for opt in (_lib.GemmOptions(_lib.GEMM_DOT2, 1, 0, 0),):
         assert lib.moat_int4_gemm_ex(FAKE, FAKE, FAKE, 9, 256, 256, ctypes.byref(opt), None, 0, None) == _lib.MOAT_ERR_INVALID
-    for opt in (_lib.GemmOptions(7, 1, 0, 0), _lib.GemmOptions(0, 1, 3, 0), _lib.GemmOptions(0, 1, 0, 4), _lib.GemmOptions(0, 1, 0, 0, 4),
-                _lib.GemmOptions(0, -1, 0, 0)):
+    for opt in (_lib.GemmOptions(7, 1, 0, 0), _lib.GemmOptions(0, 1, 5, 0), _lib.GemmOptions(0, 1, -1, 0),
+                _lib.GemmOptions(0, 1, 0, 4), _lib.GemmOptions(0, 1, 0, 0, 5), _lib.GemmOptions(0, -1, 0, 0),
+                _lib.GemmOptions(0, 1, 0, 0, 4, 3), _lib.GemmOptions(0, 1, 0, 0, 4, 8)):
         assert lib.moat_int4_gemm_ex(FAKE, FAKE, FAKE, 1, 256, 256, ctypes.byref(opt), None, 0, None) == _lib.MOAT_ERR_INVALID
         assert lib.moat_int4_gemm_ex_workspace_size(1, 256, 256, ctypes.byref(opt)) == -1
 
 
 def test_gemm_workspace_contract(lib):
     # a split-K plan needs a workspace; a missing or short one is refused before launch
-    opt = _lib.GemmOptions(_lib.GEMM_MFMA, 8, 0, 0)
+    opt = _lib.GemmOptions(_lib.GEMM_MFMA, 8, 0, 0, _lib.FRONT_LDS)  # general kernel
     size = lib.moat_int4_gemm_ex_workspace_size(1, 2048, 5504, ctypes.byref(opt))
     assert size == 64 * 1024 + 8 * 1 * 5504 * 4  # fixed counter block + partials
+    # record-stream kernel: `splits` workgroups per 256-column tile (22 tiles),
+    # two partial slots of N x 256 floats per workgroup, after the counter block
+    # (which every call leaves zero for the calls that share the workspace)
+    rec = _lib.GemmOptions(_lib.GEMM_MFMA, 8, 0, 0, _lib.FRONT_RECORDS, 1)
+    assert lib.moat_int4_gemm_ex_workspace_size(4, 2048, 5504, ctypes.byref(rec)) == 64 * 1024 + 2 * 22 * 8 * 4 * 256 * 4
+    # four tiles per workgroup: 6 tile groups, partial slots of 4 tiles
+    rec4 = _lib.GemmOptions(_lib.GEMM_MFMA, 8, 0, 0, _lib.FRONT_RECORDS, 4)
+    assert lib.moat_int4_gemm_ex_workspace_size(4, 2048, 5504, ctypes.byref(rec4)) == 64 * 1024 + 2 * 6 * 8 * 4 * 4 * 256 * 4
+    st = lib.moat_int4_gemm_ex(FAKE, FAKE, FAKE, 4, 2048, 5504, ctypes.byref(rec), None, 0, None)
+    assert st == _lib.MOAT_ERR_WORKSPACE
+    # one workgroup per tile: nothing shared, no workspace
+    one_rec = _lib.GemmOptions(_lib.GEMM_MFMA, 1, 0, 0, _lib.FRONT_RECORDS, 2)
+    assert lib.moat_int4_gemm_ex_workspace_size(4, 2048, 5504, ctypes.byref(one_rec)) == 0
     st = lib.moat_int4_gemm_ex(FAKE, FAKE, FAKE, 1, 2048, 5504, ctypes.byref(opt), None, 0, None)
     assert st == _lib.MOAT_ERR_WORKSPACE
     st = lib.moat_int4_gemm_ex(FAKE, FAKE, FAKE, 1, 2048, 5504, ctypes.byref(opt), FAKE, size - 1, None)
     assert st == _lib.MOAT_ERR_WORKSPACE
-    one = _lib.GemmOptions(_lib.GEMM_MFMA, 1, 0, 0)
+    one = _lib.GemmOptions(_lib.GEMM_MFMA, 1, 0, 0, _lib.FRONT_LDS)
     assert lib.moat_int4_gemm_ex_workspace_size(4, 2048, 2048, ctypes.byref(one)) == 0
     assert lib.moat_int4_gemm_ex_workspace_size(4, 2048, 2048, None) >= 0
     # automatic plans at the benchmark shapes: splits shrink as N grows

@@ -149,6 +149,56 @@ def test_gemm_matches_oracle_all_kernels(name, ns):
                 assert e <= TOL, (name, N, algo, splits, batch, finish, front, e)
 
 
+@pytest.mark.parametrize("K,M", [(2048, 5504), (3072, 8192), (32, 128), (64, 384), (96, 640), (32, 256),
+                                 (160, 1152)])
+def test_gemm_record_stream_kernel(K, M):
+    """The record-stream kernel (256-column tiles of whole records; rows that
+    start half-way into a record when M % 256 == 128; a 128-column last tile;
+    a short last tile group; waves with no round when K is short) at every
+    tile-group size, ring depth and stream-K split."""
+    from moat_amd.dequant import batched_int4_matmul
+    L = _lib()
+    w = O.synthetic_weights(K, M, 0.03, 11 + K + M)
+    blob = O.quantize_pack_a(w)
+    wdq = O.decode_superblocks(blob, K * M // 256).astype(np.float32).reshape(K, M)
+    blob_d = torch.from_numpy(blob.reshape(-1)).cuda()
+    rounds = K // 32
+    for N in (1, 3, 16, 17, 32):
+        x = _x(N, K, 21 + N)
+        yref = x.astype(np.float32) @ wdq
+        xd = torch.from_numpy(x).cuda()
+        for group in (1, 2, 4):
+            for depth in (1, 2, 3):
+                for splits in sorted({1, 2, min(5, rounds), min(16, rounds)}):
+                    say(f"case: records K={K} M={M} N={N} group={group} depth={depth} splits={splits}")
+                    y = batched_int4_matmul(xd, blob_d, K, M, algo=L.GEMM_MFMA, splits=splits, batch=depth,
+                                            front=L.FRONT_RECORDS, group=group)
+                    e = rel_err(y.cpu().numpy(), yref)
+                    assert e <= TOL, (K, M, N, group, depth, splits, e)
+
+
+def test_gemm_workspace_shared_between_kernels():
+    """Calls of both kernels alternate on one stream, hence one workspace:
+    the record-stream partials must leave the split-K counter block zero."""
+    from moat_amd.dequant import batched_int4_matmul
+    L = _lib()
+    K, M = 2048, 5504
+    w = O.synthetic_weights(K, M, 0.02, 77)
+    blob = O.quantize_pack_a(w)
+    wdq = O.decode_superblocks(blob, K * M // 256).astype(np.float32).reshape(K, M)
+    blob_d = torch.from_numpy(blob.reshape(-1)).cuda()
+    for N in (4, 32):
+        x = _x(N, K, 5 + N)
+        yref = x.astype(np.float32) @ wdq
+        xd = torch.from_numpy(x).cuda()
+        for rep in range(3):
+            for front, splits, finish in ((L.FRONT_RECORDS, 8, 0), (L.FRONT_LDS, 3, 1), (L.FRONT_RECORDS, 3, 0),
+                                          (L.FRONT_DIRECT, 5, 2)):
+                say(f"case: shared workspace N={N} rep={rep} front={front} splits={splits} finish={finish}")
+                y = batched_int4_matmul(xd, blob_d, K, M, algo=L.GEMM_MFMA, splits=splits, finish=finish, front=front)
+                assert rel_err(y.cpu().numpy(), yref) <= TOL, (N, rep, front, splits, finish)
+
+
 def test_gemm_equals_stacked_gemv():
     """GEMM(N) == N single-row products (antigravity-engine/tests/test_batched_speed.py:55-86)."""
     from moat_amd.dequant import batched_int4_matmul
