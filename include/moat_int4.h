@@ -98,8 +98,8 @@ typedef struct moat_int4_gemm_options {
   int32_t algo;   /* MOAT_GEMM_*: 0 automatic, 1 dot2 (n <= 8), 2 MFMA */
   int32_t splits; /* K slices per column tile, >= 1; 0 automatic (record-stream kernel: workgroups
                      per tile group, each taking an equal run of (tile group, round) items) */
-  int32_t batch;  /* 32-row rounds a wave has in flight: 1..4 (general kernel: 1, 2 or 4 issued
-                     together; record-stream kernel: ring depth, 3 at most); 0 automatic */
+  int32_t batch;  /* 32-row rounds a wave has in flight (general kernel: 1, 2 or 4 issued
+                     together; record-stream kernel: ring depth 1..5); 0 automatic */
   int32_t finish; /* split-K hand-off, MOAT_FINISH_*; 0 automatic */
   int32_t front;  /* weight loads, MOAT_FRONT_*; 0 automatic */
   int32_t group;  /* record-stream kernel: adjacent 256-column tiles per workgroup, 1, 2 or 4

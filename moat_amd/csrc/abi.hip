@@ -70,7 +70,7 @@ bool gemm_shape_ok(int32_t n, int32_t k, int32_t m) {
 bool options_ok(const moat_int4_gemm_options* o, int32_t n) {
   if (!o) return true;
   if (o->algo < 0 || o->algo > 2 || o->splits < 0) return false;
-  if (o->batch < 0 || o->batch > 4) return false;
+  if (o->batch < 0 || o->batch > 5) return false;
   if (o->finish < 0 || o->finish > 3) return false;
   if (o->front < 0 || o->front > 4) return false;
   if (o->group != 0 && o->group != 1 && o->group != 2 && o->group != 4) return false;
@@ -123,7 +123,10 @@ GemmPlan plan_gemm(int32_t n, int32_t k, int32_t m, const moat_int4_gemm_options
     p.splits = (int)wgs;
     p.group = group;
     p.batch = opt.batch ? opt.batch : (n <= 16 ? 3 : 2);  // ring depth (LDS: 4 waves x depth x 6 or 7 KB)
-    p.finish = 2;                          // shared tile groups are summed by the fix-up kernel
+    // shared tile groups: summed by a fix-up kernel (the default, measured
+    // as fast or faster at every N) or, with MOAT_FINISH_DEVICE_ATOMICS or
+    // MOAT_FINISH_FENCES, by the last contributing workgroup
+    p.finish = (opt.finish == MOAT_FINISH_AUTO || opt.finish == MOAT_FINISH_SECOND_KERNEL) ? 2 : 0;
     p.front = 3;
     // the partials follow the fixed counter block, which other calls sharing
     // the workspace rely on staying zero

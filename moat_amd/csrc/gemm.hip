@@ -571,18 +571,21 @@ __global__ void __launch_bounds__(kThreads) int4_gemm_kernel(GemmParams P) {
 //    tile's groups 0-3 have their scales at bytes 8..15), payload chunks 4-7
 //    of s, the header of s+1 (groups 4-7 at bytes 0..7) and payload chunks
 //    0-3 of s+1, the last nine being one contiguous 144-byte window.
-// A round (32 rows) is therefore 32 x 10 chunk slots (5 KB), plus the
-// round's X slice (16 rows x 32 fp16 per 16-row block of X).  Both are moved
+// A round (32 rows) therefore needs at most 10 chunks per row; the stage
+// gives each row 11 chunk slots (176 bytes: rows 8 apart, which the four
+// lane groups of an LDS read address together, then fall on different
+// banks), 6 KB per round, plus the round's X slice (16 rows x 32 fp16 per
+// 16-row block of X).  Both are moved
 // with global_load_lds (16 bytes per lane, straight into LDS) into a
 // per-wave ring of kDepth stages: the wave keeps kDepth - 1 rounds in flight
 // while it computes one, and waits for a round with an explicit vmcnt.
 // Whole records per row touch the fewest 128-byte lines per instruction of
 // any layout of this stream.
 constexpr int kRecCols = 256;
-constexpr int kRecSlotsPerRow = 10;
-constexpr int kRecRowBytes = 16 * kRecSlotsPerRow;          // 160
-constexpr int kRecWeightBytes = kRoundRows * kRecRowBytes;  // 5120: 5 loads of 64 x 16 bytes
-constexpr int kRecWeightLoads = kRecWeightBytes / 1024;
+constexpr int kRecSlotsPerRow = 11;
+constexpr int kRecRowBytes = 16 * kRecSlotsPerRow;                                  // 176
+constexpr int kRecWeightLoads = (kRoundRows * kRecRowBytes + 1023) / 1024;          // 6 loads of 64 x 16 bytes
+constexpr int kRecWeightBytes = kRecWeightLoads * 1024;                             // 6144
 
 template <int NR>
 struct RecGeom {
@@ -591,11 +594,12 @@ struct RecGeom {
 };
 
 // Source offsets (round 0) of a lane's weight slots.  Slot s = 64*i + lane
-// carries chunk c = s % 10 of row s / 10 and lands at byte 16*s of the stage,
-// so row t starts at byte 160*t.  Slots that carry nothing the tile needs
-// (chunk 9 of an aligned row, groups past M in the last tile) re-load the
-// row's first header chunk: every round issues the same instructions, which
-// keeps the vmcnt arithmetic exact, and every address stays inside the stream.
+// carries chunk c = s % 11 of row s / 11 and lands at byte 16*s of the stage,
+// so row t starts at byte 176*t.  Slots that carry nothing the tile needs
+// (chunk 9 of an aligned row, chunk 10, the slots past row 31, groups past M
+// in the last tile) re-load the row's first header chunk: every round issues
+// the same instructions, which keeps the vmcnt arithmetic exact, and every
+// address stays inside the stream.
 struct RecSlots {
   uint32_t off[kRecWeightLoads];
 };
@@ -604,7 +608,8 @@ __device__ __forceinline__ void rec_slots(RecSlots& s, int lane, int tile, int m
 #pragma unroll
   for (int i = 0; i < kRecWeightLoads; ++i) {
     const int slot = 64 * i + lane;
-    const int row = slot / kRecSlotsPerRow, c = slot % kRecSlotsPerRow;
+    const int row = min(slot / kRecSlotsPerRow, kRoundRows - 1);
+    const int c = slot < kRoundRows * kRecSlotsPerRow ? slot % kRecSlotsPerRow : kRecSlotsPerRow - 1;
     const uint32_t flat = (uint32_t)row * (uint32_t)m + (uint32_t)(kRecCols * tile);
     const uint32_t head = (flat >> 8) * kSbBytes;
     // record-aligned row: header, then payload chunk c-1 at 16*c
@@ -733,13 +738,37 @@ __device__ __forceinline__ int red_pos(int row, int jj, int u) {
   return row * kRecCols + 16 * jj + 4 * ((u + (jj >> 2)) & 3);
 }
 
+// Device-coherent (agent scope) vector accesses for the in-kernel hand-off:
+// sc1 stores write through and sc1 loads read past the per-XCD L2s, the
+// same cache policy as relaxed agent-scope atomics, 16 bytes at a time.
+__device__ __forceinline__ void store_sc1(float* p, float4_t v) {
+  asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
+}
+
+// Eight independent sc1 loads in flight, then one wait.
+__device__ __forceinline__ void load8_sc1(float4_t (&t)[8], const float* const (&a)[8]) {
+  asm volatile(
+      "global_load_dwordx4 %0, %8, off sc1\n\t"
+      "global_load_dwordx4 %1, %9, off sc1\n\t"
+      "global_load_dwordx4 %2, %10, off sc1\n\t"
+      "global_load_dwordx4 %3, %11, off sc1\n\t"
+      "global_load_dwordx4 %4, %12, off sc1\n\t"
+      "global_load_dwordx4 %5, %13, off sc1\n\t"
+      "global_load_dwordx4 %6, %14, off sc1\n\t"
+      "global_load_dwordx4 %7, %15, off sc1\n\t"
+      "s_waitcnt vmcnt(0)"
+      : "=&v"(t[0]), "=&v"(t[1]), "=&v"(t[2]), "=&v"(t[3]), "=&v"(t[4]), "=&v"(t[5]), "=&v"(t[6]), "=&v"(t[7])
+      : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(a[4]), "v"(a[5]), "v"(a[6]), "v"(a[7])
+      : "memory");
+}
+
 // Output of a tile group: tile tl of the group sums `nslots` LDS slots
 // (slot s of tile tl at red + (tl * nslots + s) * per_slot) and goes to Y
 // (part == nullptr) or to the partial slot part + tl * per_slot.  The whole
 // workgroup stores, one 4-column quad per thread and step.
 template <int kC>
 __device__ __forceinline__ void rec_store(const GemmParams& P, const float* red, int per_slot, int nslots, int tg,
-                                          float* part) {
+                                          float* part, bool coherent) {
   const int total = kC * P.n * 64;
   for (int idx = threadIdx.x; idx < total; idx += kThreads) {
     const int tl = idx / (P.n * 64);
@@ -752,7 +781,9 @@ __device__ __forceinline__ void rec_store(const GemmParams& P, const float* red,
     float4_t v = *reinterpret_cast<const float4_t*>(base);
     if (nslots > 1) v += *reinterpret_cast<const float4_t*>(base + per_slot);
     if (part) {
-      *reinterpret_cast<float4_t*>(part + tl * per_slot + row * kRecCols + 4 * qd) = v;
+      float* pp = part + tl * per_slot + row * kRecCols + 4 * qd;
+      if (coherent) store_sc1(pp, v);
+      else *reinterpret_cast<float4_t*>(pp) = v;
     } else {
       float* yp = P.y + (int64_t)row * P.m + m0 + 4 * qd;
       if (P.y_vec) {
@@ -765,6 +796,60 @@ __device__ __forceinline__ void rec_store(const GemmParams& P, const float* red,
   }
 }
 
+// In-kernel hand-off of a shared tile group: this workgroup's partials are
+// written (sc1) and acknowledged, then one agent-scope counter per group
+// counts the contributors; the last one adds every contributor's partials in
+// workgroup order (sc1 loads, eight in flight), writes Y and clears the
+// counter for the next call.
+template <int kC>
+__device__ __forceinline__ void rec_handoff(const GemmParams& P, int tg) {
+  __shared__ int s_last;
+  asm volatile("s_waitcnt vmcnt(0)" : : : "memory");  // this thread's partial stores are complete
+  __syncthreads();
+  const int item0 = tg * P.rounds;
+  const int p0 = streamk_owner(P, item0), p1 = streamk_owner(P, item0 + P.rounds - 1);
+  if (threadIdx.x == 0) {
+    const uint32_t prev = __hip_atomic_fetch_add(&P.counters[tg], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = prev == (uint32_t)(p1 - p0);
+  }
+  __syncthreads();
+  if (!s_last) return;
+  const int per_slot = P.n * kRecCols;
+  const int total = kC * P.n * 64;
+  for (int idx = threadIdx.x; idx < total; idx += kThreads) {
+    const int tl = idx / (P.n * 64);
+    const int w = idx - tl * P.n * 64;
+    const int row = w >> 6, qd = w & 63;
+    const int m0 = (tg * kC + tl) * kRecCols;
+    if (m0 + 4 * qd >= P.m) continue;
+    const int64_t off = (int64_t)tl * per_slot + row * kRecCols + 4 * qd;
+    float4_t v = {0.f, 0.f, 0.f, 0.f};
+    for (int p8 = p0; p8 <= p1; p8 += 8) {
+      const float* a[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int pp = min(p8 + i, p1);  // past the end: re-read the last one, added as 0 below
+        const int lo_p = pp * P.items_base + min(pp, P.items_rem);
+        const int pslot = 2 * pp + (lo_p < item0 ? 1 : 0);
+        a[i] = P.partials + (int64_t)pslot * kC * per_slot + off;
+      }
+      float4_t t[8];
+      load8_sc1(t, a);
+#pragma unroll
+      for (int i = 0; i < 8; ++i)  // in workgroup order
+        if (p8 + i <= p1) v += t[i];
+    }
+    float* yp = P.y + (int64_t)row * P.m + m0 + 4 * qd;
+    if (P.y_vec) {
+      *reinterpret_cast<float4_t*>(yp) = v;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) yp[e] = v[e];
+    }
+  }
+  if (threadIdx.x == 0) __hip_atomic_store(&P.counters[tg], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 template <int NR, int kDepth, int kC>
 __global__ void __launch_bounds__(kThreads) int4_gemm_records_kernel(GemmParams P) {
   using G = RecGeom<NR>;
@@ -773,7 +858,8 @@ __global__ void __launch_bounds__(kThreads) int4_gemm_records_kernel(GemmParams 
   // fetch every argument now, in one batch of scalar loads, rather than at
   // first use (each late load is another serial trip to memory)
   asm volatile("" : : "s"(P.x), "s"(P.sb), "s"(P.y), "s"(P.partials), "s"(P.n), "s"(P.k), "s"(P.m),
-               "s"(P.rounds), "s"(P.shift), "s"(P.y_vec), "s"(P.items_base), "s"(P.items_rem), "s"(P.tiles));
+               "s"(P.rounds), "s"(P.shift), "s"(P.y_vec), "s"(P.items_base), "s"(P.items_rem), "s"(P.tiles),
+               "s"(P.counters), "s"(P.finish));
   const int lane = threadIdx.x & 63;
   // wave index as a scalar: the round loop below is then uniform control flow
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -791,15 +877,17 @@ __global__ void __launch_bounds__(kThreads) int4_gemm_records_kernel(GemmParams 
     rd.pay[1] = rd.pay[0];
     rd.sc[1] = rd.sc[0];
   }
-  rd.x = 64 * j + 16 * (q ^ (j & 3));
+  rd.x = 64 * j + 16 * (q ^ (j & 3) ^ ((j >> 2) & 3));
   // X slice loads: lane l fetches row 16*nt + l/4 (rows past N repeat row N-1;
   // their products land in output rows that are never stored), 8 fp16 at
-  // column 8 * ((l & 3) ^ ((l >> 2) & 3)) of the round
+  // column 8 * ((l & 3) ^ ((l >> 2) & 3) ^ ((l >> 4) & 3)) of the round: the
+  // read-back (lane (q, j): row j, columns 8q..8q+7) then spreads any 8
+  // consecutive lanes over 8 different 16-byte bank groups
   uint32_t xoff[NR];
 #pragma unroll
   for (int nt = 0; nt < NR; ++nt) {
     const int row = min(16 * nt + (lane >> 2), P.n - 1);
-    const int chunk = (lane & 3) ^ ((lane >> 2) & 3);
+    const int chunk = (lane & 3) ^ ((lane >> 2) & 3) ^ ((lane >> 4) & 3);
     xoff[nt] = (uint32_t)(2 * (row * P.k + 8 * chunk));
   }
   // workgroup ids are dealt round-robin to the 8 XCDs: give each XCD one
@@ -850,7 +938,9 @@ __global__ void __launch_bounds__(kThreads) int4_gemm_records_kernel(GemmParams 
         wait_vmcnt<(kDepth - 1) * G::kLoads>();
       } else {
         const int after = cnt - 1 - i;  // rounds issued after round i: 0 .. kDepth - 2
-        if (kDepth >= 3 && after == 2) wait_vmcnt<(kDepth >= 3 ? 2 * G::kLoads : 0)>();
+        if (kDepth >= 5 && after == 4) wait_vmcnt<(kDepth >= 5 ? 4 * G::kLoads : 0)>();
+        else if (kDepth >= 4 && after == 3) wait_vmcnt<(kDepth >= 4 ? 3 * G::kLoads : 0)>();
+        else if (kDepth >= 3 && after == 2) wait_vmcnt<(kDepth >= 3 ? 2 * G::kLoads : 0)>();
         else if (kDepth >= 2 && after == 1) wait_vmcnt<(kDepth >= 2 ? G::kLoads : 0)>();
         else wait_vmcnt<0>();
       }
@@ -891,8 +981,10 @@ __global__ void __launch_bounds__(kThreads) int4_gemm_records_kernel(GemmParams 
     }
     const bool whole = r0 == 0 && r1 == P.rounds;
     const int pslot = 2 * p + (seg_lo == lo ? 0 : 1);
-    rec_store<kC>(P, red, per_slot, kSlots, tg,
-                  whole ? nullptr : P.partials + (int64_t)pslot * kC * per_slot);
+    const bool in_kernel = P.finish != kFinishSecondKernel;
+    rec_store<kC>(P, red, per_slot, kSlots, tg, whole ? nullptr : P.partials + (int64_t)pslot * kC * per_slot,
+                  in_kernel);
+    if (!whole && in_kernel) rec_handoff<kC>(P, tg);
     __syncthreads();  // LDS is the next segment's ring
     seg_lo = seg_hi;
   }
@@ -1003,11 +1095,16 @@ static hipError_t launch_front(const GemmParams& P, int algo, int batch, hipStre
   return launch_gemm_variant<1, kFront>(P, algo, stream);
 }
 
+// LDS a workgroup may take on gfx950 (160 KB), less room for the kernels'
+// static __shared__ words.
+constexpr size_t kMaxDynamicLds = 156 * 1024;
+
 template <int NR, int kDepth, int kC>
 static hipError_t launch_records_one(const GemmParams& P, int wgs, hipStream_t stream) {
   constexpr int kShare = kWaves / kC;
   const size_t ring = (size_t)kWaves * kDepth * RecGeom<NR>::kStageBytes;
   const size_t red = (size_t)kC * (kShare == 4 ? 2 : 1) * P.n * kRecCols * sizeof(float);
+  if (ring > kMaxDynamicLds || red > kMaxDynamicLds) return hipErrorInvalidValue;  // never launch past the LDS
   hipLaunchKernelGGL((int4_gemm_records_kernel<NR, kDepth, kC>), dim3(wgs), dim3(kThreads), ring > red ? ring : red,
                      stream, P);
   return hipGetLastError();
@@ -1015,7 +1112,12 @@ static hipError_t launch_records_one(const GemmParams& P, int wgs, hipStream_t s
 
 template <int NR, int kC>
 static hipError_t launch_records_depth(const GemmParams& P, int wgs, int depth, hipStream_t stream) {
-  if (depth >= 3) return launch_records_one<NR, 3, kC>(P, wgs, stream);
+  // the ring must fit: clamp the depth (4 waves x depth stages)
+  const int max_depth = (int)(kMaxDynamicLds / ((size_t)kWaves * RecGeom<NR>::kStageBytes));
+  if (depth > max_depth) depth = max_depth;
+  if (depth >= 5) return launch_records_one<NR, 5, kC>(P, wgs, stream);
+  if (depth == 4) return launch_records_one<NR, 4, kC>(P, wgs, stream);
+  if (depth == 3) return launch_records_one<NR, 3, kC>(P, wgs, stream);
   if (depth == 2) return launch_records_one<NR, 2, kC>(P, wgs, stream);
   return launch_records_one<NR, 1, kC>(P, wgs, stream);
 }
@@ -1068,7 +1170,8 @@ hipError_t launch_gemm(int algo, const uint16_t* x, const uint8_t* sb, float* y,
       P.y_vec = ((reinterpret_cast<uintptr_t>(y) & 15) == 0) ? 1 : 0;
       e = P.n <= 16 ? launch_records<1>(P, wgs, batch, group_tiles, stream)
                     : launch_records<2>(P, wgs, batch, group_tiles, stream);
-      if (e != hipSuccess || !gemm_records_shares_tiles(k, m, group_tiles, wgs)) return e;
+      if (e != hipSuccess || !gemm_records_shares_tiles(k, m, group_tiles, wgs) || finish != kFinishSecondKernel)
+        return e;
       const int quads = P.tiles * P.n * 64;
       int blocks = (quads + 255) / 256;
       if (blocks > 2048) blocks = 2048;

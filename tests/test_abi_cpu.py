@@ -77,7 +77,7 @@ def test_gemm_rejects_null_and_misaligned(lib):
     # dot2 kernel only up to N = 8; unknown algo / batch / finish values are refused
     for opt in (_lib.GemmOptions(_lib.GEMM_DOT2, 1, 0, 0),):
         assert lib.moat_int4_gemm_ex(FAKE, FAKE, FAKE, 9, 256, 256, ctypes.byref(opt), None, 0, None) == _lib.MOAT_ERR_INVALID
-    for opt in (_lib.GemmOptions(7, 1, 0, 0), _lib.GemmOptions(0, 1, 5, 0), _lib.GemmOptions(0, 1, -1, 0),
+    for opt in (_lib.GemmOptions(7, 1, 0, 0), _lib.GemmOptions(0, 1, 6, 0), _lib.GemmOptions(0, 1, -1, 0),
                 _lib.GemmOptions(0, 1, 0, 4), _lib.GemmOptions(0, 1, 0, 0, 5), _lib.GemmOptions(0, -1, 0, 0),
                 _lib.GemmOptions(0, 1, 0, 0, 4, 3), _lib.GemmOptions(0, 1, 0, 0, 4, 8)):
         assert lib.moat_int4_gemm_ex(FAKE, FAKE, FAKE, 1, 256, 256, ctypes.byref(opt), None, 0, None) == _lib.MOAT_ERR_INVALID

@@ -155,7 +155,8 @@ def test_gemm_record_stream_kernel(K, M):
     """The record-stream kernel (256-column tiles of whole records; rows that
     start half-way into a record when M % 256 == 128; a 128-column last tile;
     a short last tile group; waves with no round when K is short) at every
-    tile-group size, ring depth and stream-K split."""
+    tile-group size, ring depth, stream-K split and hand-off (last workgroup
+    in the kernel, or the fix-up kernel)."""
     from moat_amd.dequant import batched_int4_matmul
     L = _lib()
     w = O.synthetic_weights(K, M, 0.03, 11 + K + M)
@@ -168,13 +169,15 @@ def test_gemm_record_stream_kernel(K, M):
         yref = x.astype(np.float32) @ wdq
         xd = torch.from_numpy(x).cuda()
         for group in (1, 2, 4):
-            for depth in (1, 2, 3):
+            for depth in (1, 2, 3, 5):
                 for splits in sorted({1, 2, min(5, rounds), min(16, rounds)}):
-                    say(f"case: records K={K} M={M} N={N} group={group} depth={depth} splits={splits}")
-                    y = batched_int4_matmul(xd, blob_d, K, M, algo=L.GEMM_MFMA, splits=splits, batch=depth,
-                                            front=L.FRONT_RECORDS, group=group)
-                    e = rel_err(y.cpu().numpy(), yref)
-                    assert e <= TOL, (K, M, N, group, depth, splits, e)
+                    for finish in (L.FINISH_AUTO, L.FINISH_SECOND_KERNEL):
+                        say(f"case: records K={K} M={M} N={N} group={group} depth={depth} splits={splits} "
+                            f"finish={finish}")
+                        y = batched_int4_matmul(xd, blob_d, K, M, algo=L.GEMM_MFMA, splits=splits, batch=depth,
+                                                finish=finish, front=L.FRONT_RECORDS, group=group)
+                        e = rel_err(y.cpu().numpy(), yref)
+                        assert e <= TOL, (K, M, N, group, depth, splits, finish, e)
 
 
 def test_gemm_workspace_shared_between_kernels():
@@ -273,14 +276,16 @@ def test_gemm_split_k_handoff_is_deterministic():
     from moat_amd.dequant import batched_int4_matmul
     K, M, _, blob = workload("ffn 2048x5504")
     blob_d = torch.from_numpy(blob.reshape(-1)).cuda()
-    for N in (1, 4, 32):
-        x = torch.from_numpy(_x(N, K, 3)).cuda()
-        ref = batched_int4_matmul(x, blob_d, K, M, algo=2, splits=16, finish=3)
-        for finish in (1, 2, 3):
-            say(f"case: split-K hand-off N={N} finish={finish}")
-            for _ in range(20):
-                y = batched_int4_matmul(x, blob_d, K, M, algo=2, splits=16, finish=finish)
-                assert torch.equal(y, ref), (N, finish)
+    L = _lib()
+    for front in (L.FRONT_RECORDS, L.FRONT_LDS):
+        for N in (1, 4, 32):
+            x = torch.from_numpy(_x(N, K, 3)).cuda()
+            ref = batched_int4_matmul(x, blob_d, K, M, algo=2, splits=16, finish=3, front=front)
+            for finish in (1, 2, 3):
+                say(f"case: split-K hand-off front={front} N={N} finish={finish}")
+                for _ in range(20):
+                    y = batched_int4_matmul(x, blob_d, K, M, algo=2, splits=16, finish=finish, front=front)
+                    assert torch.equal(y, ref), (front, N, finish)
 
 
 def test_gemm_n_above_32_is_sliced():

@@ -18,9 +18,9 @@ payload and scale of its rows.  It checks that
 import numpy as np
 import pytest
 
-SLOTS_PER_ROW = 10
-ROW_BYTES = 160
-WEIGHT_LOADS = 5
+SLOTS_PER_ROW = 11
+ROW_BYTES = 176
+WEIGHT_LOADS = 6
 
 
 def rec_slots(lane, tile, m, groups):
@@ -28,6 +28,8 @@ def rec_slots(lane, tile, m, groups):
     for i in range(WEIGHT_LOADS):
         slot = 64 * i + lane
         row, c = divmod(slot, SLOTS_PER_ROW)
+        if row > 31:
+            row, c = 31, SLOTS_PER_ROW - 1
         flat = row * m + 256 * tile
         head = (flat >> 8) * 144
         off = head
@@ -72,7 +74,7 @@ def check_shape(K, M, n=32, tiles_to_check=None):
         lane_offs = [rec_slots(l, tile, M, groups) for l in range(64)]
         for r in {0, rounds // 2, rounds - 1}:
             base = r * 18 * M
-            stage = np.zeros(5120, dtype=np.uint8)
+            stage = np.zeros(1024 * WEIGHT_LOADS, dtype=np.uint8)
             for lane in range(64):
                 for i, off in enumerate(lane_offs[lane]):
                     a = base + off
@@ -94,20 +96,20 @@ def check_shape(K, M, n=32, tiles_to_check=None):
                     assert np.array_equal(got, stream[pay:pay + 8]), (K, M, tile, r, t, j)
                     got_s = stage[ROW_BYTES * t + so:ROW_BYTES * t + so + 2]
                     assert np.array_equal(got_s, stream[sca:sca + 2]), (K, M, tile, r, t, j, "scale")
-    # X slices: lane l copies row min(16nt + l/4, n-1), chunk (l&3)^((l>>2)&3)
+    # X slices: lane l copies row min(16nt + l/4, n-1), chunk (l&3)^((l>>2)&3)^((l>>4)&3)
     xbytes = 2 * n * K
     for nt in range(2 if n > 16 else 1):
         pos = {}
         for lane in range(64):
             row = min(16 * nt + (lane >> 2), n - 1)
-            chunk = (lane & 3) ^ ((lane >> 2) & 3)
+            chunk = (lane & 3) ^ ((lane >> 2) & 3) ^ ((lane >> 4) & 3)
             for r in (0, rounds - 1):
                 a = 2 * (row * K + 8 * chunk) + 64 * r
                 assert 0 <= a and a + 16 <= xbytes
             pos[16 * lane] = (row, chunk)
         for q in range(4):
             for j in range(16):
-                rx = 64 * j + 16 * (q ^ (j & 3))
+                rx = 64 * j + 16 * (q ^ (j & 3) ^ ((j >> 2) & 3))
                 row, chunk = pos[rx]
                 assert chunk == q and row == min(16 * nt + j, n - 1)
 
