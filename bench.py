@@ -89,6 +89,41 @@ def cpu_baseline(K, M, ns, blob, budget_s: float):
     }
 
 
+def traffic_from_counters(fetch_csv: str, write_csv: str, config: str, n: int) -> dict:
+    """HBM bytes per launch of the GEMM kernels from two rocprofv3 --pmc runs
+    of this script (FETCH_SIZE, then WRITE_SIZE, CSV output, ``--ns n``).
+    Each counter is scaled by what it reads for the largest plain copy of the
+    same run: the clones of the weight stream, whose size is known (every
+    clone reads and writes exactly the record bytes).  Returns the entry
+    written to profiles/traffic_<config>.json."""
+    import csv
+    K, M = CONFIGS[config][:2]
+    sb_bytes = 144 * K * M // 256
+
+    def per_kernel(path, counter):
+        rows = [r for r in csv.DictReader(open(path)) if r["Counter_Name"] == counter]
+        copies = [float(r["Counter_Value"]) for r in rows if "copyBuffer" in r["Kernel_Name"]]
+        scale = sb_bytes / (max(copies) * 1024.0)  # counter reads KiB
+        out = {}
+        for r in rows:
+            name = r["Kernel_Name"]
+            if "gemm" in name or "fixup" in name or "splitk_sum" in name:
+                key = name.split("(")[0].replace("void ", "")
+                out.setdefault(key, []).append(float(r["Counter_Value"]) * 1024.0 * scale)
+        med = {k: float(np.median(v)) for k, v in out.items()}
+        return med, scale
+
+    fetch, fs = per_kernel(fetch_csv, "FETCH_SIZE")
+    write, ws = per_kernel(write_csv, "WRITE_SIZE")
+    kernels = {k: {"read_bytes": round(fetch.get(k, 0.0)), "written_bytes": round(write.get(k, 0.0))}
+               for k in sorted(set(fetch) | set(write))}
+    main_k = max(kernels, key=lambda k: kernels[k]["read_bytes"])
+    total = kernels[main_k]["read_bytes"] + kernels[main_k]["written_bytes"]
+    return {"n": n, "traffic": total, "kernel": main_k, "algorithmic_bytes": algo_bytes(n, K, M),
+            "kernels": kernels, "scale": {"FETCH_SIZE": round(fs, 4), "WRITE_SIZE": round(ws, 4)},
+            "calibration": f"largest __amd_rocclr_copyBuffer of the run = one clone of the {sb_bytes}-byte record stream"}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -103,8 +138,23 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--batch", type=int, default=0, help="rounds of loads issued together (0 auto)")
     ap.add_argument("--finish", type=int, default=0, help="split-K hand-off (0 auto, 1 atomics, 2 fences, 3 kernel)")
-    ap.add_argument("--front", type=int, default=0, help="load front end (0 auto, 1 LDS-staged, 2 direct, 3 LDS DMA)")
+    ap.add_argument("--front", type=int, default=0,
+                    help="load front end (0 auto, 1 LDS-staged, 2 direct, 3 LDS DMA, 4 record stream)")
+    ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"), default=None,
+                    help="no GPU run: turn two rocprofv3 --pmc counter CSVs (FETCH_SIZE, WRITE_SIZE) of "
+                         "`bench.py --ns N` into profiles/traffic_<config>.json")
     args = ap.parse_args()
+
+    if args.traffic_from:
+        n = int(args.ns.split(",")[0]) if args.ns else max(CONFIGS[args.config][5])
+        entry = traffic_from_counters(args.traffic_from[0], args.traffic_from[1], args.config, n)
+        path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", f"traffic_{args.config}.json")
+        data = json.load(open(path)) if os.path.exists(path) else {}
+        data[str(n)] = entry
+        with open(path, "w") as f:
+            json.dump(data, f, indent=1)
+        print(json.dumps(entry))
+        return 0
 
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})",
@@ -212,7 +262,8 @@ def main() -> int:
         "unit": "GB/s",
         "frac": per_n[dom]["roofline_frac"],
         "traffic": None,
-        "kernel": f"int4 gemm N={dom} ({per_n[dom]['us_per_call']} us/launch, {per_n[dom]['algo_bytes']} algorithmic B)",
+        "kernel": (f"int4 gemm N={dom}: {per_n[dom]['algo_bytes']} algorithmic B per call / "
+                   f"{per_n[dom]['us_per_call']} us per call (main kernel + fix-up of shared tiles)"),
     }
     traffic_file = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                                 f"traffic_{args.config}.json")
@@ -220,7 +271,8 @@ def main() -> int:
         with open(traffic_file) as f:
             tr = json.load(f).get(str(dom))
         if tr is not None:
-            roof["traffic"] = tr
+            roof["traffic"] = tr["traffic"]
+            roof["traffic_source"] = f"profiles/traffic_{args.config}.json ({tr['kernel']})"
 
     cpu = None
     if not args.no_cpu_baseline:

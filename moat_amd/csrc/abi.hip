@@ -27,6 +27,7 @@ int gemm_rounds(int k);
 bool gemm_records_eligible(int k, int m);
 int gemm_records_tiles(int m);
 int gemm_records_groups(int m, int group_tiles);
+size_t gemm_records_lds(int n, int depth, int group_tiles);
 bool gemm_records_shares_tiles(int k, int m, int group_tiles, int wgs);
 hipError_t launch_gemm(int algo, const uint16_t* x, const uint8_t* sb, float* y, int n, int k, int m, int splits,
                        int batch, int finish, int front, int group, float* partials, uint32_t* counters,
@@ -105,13 +106,25 @@ GemmPlan plan_gemm(int32_t n, int32_t k, int32_t m, const moat_int4_gemm_options
     const int group = opt.group ? opt.group : 1;
     const int groups = moat::gemm_records_groups(m, group);
     const int64_t tiles_r = moat::gemm_records_tiles(m);
+    const int depth = opt.batch ? opt.batch : (n <= 16 ? 3 : 2);  // ring depth (LDS: 4 waves x depth x 7 or 8 KB)
     int64_t splits;
     if (opt.splits > 0) {
       splits = opt.splits;
     } else {
       splits = (tiles_r * rounds / 8 + groups / 2) / groups;  // ~2 rounds per wave
-      const int64_t cap_wgs = 512 / groups > 0 ? 512 / groups : 1;
+      if (splits > 8) splits = 8;  // beyond 8 the hand-off costs more than the shorter loop saves
+      // no more workgroups than the 256 CUs hold at once (a second wave of
+      // workgroups would double the time)
+      const int64_t per_cu = (int64_t)(160 * 1024) / (int64_t)moat::gemm_records_lds(n, depth, group);
+      const int64_t resident = 256 * (per_cu > 0 ? per_cu : 1);
+      const int64_t cap_wgs = resident / groups > 0 ? resident / groups : 1;
       if (splits > cap_wgs) splits = cap_wgs;
+      // above 16 rows the partial sums (N x 256 floats per workgroup) weigh:
+      // stop at about one workgroup per CU
+      if (n > 16) {
+        const int64_t one_per_cu = 256 / groups > 2 ? 256 / groups : 2;
+        if (splits > one_per_cu) splits = one_per_cu;
+      }
       int64_t by_traffic = k / (16 * n);
       if (by_traffic < 2) by_traffic = 2;
       if (splits > by_traffic) splits = by_traffic;
@@ -122,7 +135,7 @@ GemmPlan plan_gemm(int32_t n, int32_t k, int32_t m, const moat_int4_gemm_options
     if (wgs > items) wgs = items;
     p.splits = (int)wgs;
     p.group = group;
-    p.batch = opt.batch ? opt.batch : (n <= 16 ? 3 : 2);  // ring depth (LDS: 4 waves x depth x 6 or 7 KB)
+    p.batch = depth;
     // shared tile groups: summed by a fix-up kernel (the default, measured
     // as fast or faster at every N) or, with MOAT_FINISH_DEVICE_ATOMICS or
     // MOAT_FINISH_FENCES, by the last contributing workgroup

@@ -582,6 +582,9 @@ __global__ void __launch_bounds__(kThreads) int4_gemm_kernel(GemmParams P) {
 // Whole records per row touch the fewest 128-byte lines per instruction of
 // any layout of this stream.
 constexpr int kRecCols = 256;
+// LDS a workgroup may take on gfx950 (160 KB), less room for the kernels'
+// static __shared__ words.
+constexpr size_t kMaxDynamicLds = 156 * 1024;
 constexpr int kRecSlotsPerRow = 11;
 constexpr int kRecRowBytes = 16 * kRecSlotsPerRow;                                  // 176
 constexpr int kRecWeightLoads = (kRoundRows * kRecRowBytes + 1023) / 1024;          // 6 loads of 64 x 16 bytes
@@ -1095,10 +1098,6 @@ static hipError_t launch_front(const GemmParams& P, int algo, int batch, hipStre
   return launch_gemm_variant<1, kFront>(P, algo, stream);
 }
 
-// LDS a workgroup may take on gfx950 (160 KB), less room for the kernels'
-// static __shared__ words.
-constexpr size_t kMaxDynamicLds = 156 * 1024;
-
 template <int NR, int kDepth, int kC>
 static hipError_t launch_records_one(const GemmParams& P, int wgs, hipStream_t stream) {
   constexpr int kShare = kWaves / kC;
@@ -1130,6 +1129,16 @@ static hipError_t launch_records(const GemmParams& P, int wgs, int depth, int gr
 }
 
 bool gemm_records_eligible(int k, int m) { return (m % 128) == 0 && (k % kRoundRows) == 0; }
+
+// Dynamic LDS of one record-stream workgroup (after the depth clamp).
+size_t gemm_records_lds(int n, int depth, int group_tiles) {
+  const size_t stage = n <= 16 ? RecGeom<1>::kStageBytes : RecGeom<2>::kStageBytes;
+  const int max_depth = (int)(kMaxDynamicLds / (kWaves * stage));
+  if (depth > max_depth) depth = max_depth;
+  const size_t ring = (size_t)kWaves * depth * stage;
+  const size_t red = (size_t)group_tiles * (group_tiles == 1 ? 2 : 1) * n * kRecCols * sizeof(float);
+  return ring > red ? ring : red;
+}
 int gemm_records_tiles(int m) { return (m + kRecCols - 1) / kRecCols; }
 int gemm_records_groups(int m, int group_tiles) { return (gemm_records_tiles(m) + group_tiles - 1) / group_tiles; }
 
