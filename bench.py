@@ -223,11 +223,14 @@ def main() -> int:
         e1.synchronize()
         return e0.elapsed_time(e1) * 1e3  # us
 
-    # per-N table: `calls` launches per N, each on the next weight copy
+    # per-N table: `calls` launches per N, each on the next weight copy, after
+    # about 20 ms of the same launches (the GPU leaves its idle clocks)
     per_n = {}
     for N in ns:
         g = capture([(N, i) for i in range(copies)])
         reps = max(1, args.calls // copies)
+        warm_us = timed([g], 1)
+        timed([g], max(1, int(20000 / max(warm_us, 1.0))))
         us = timed([g], reps) / (reps * copies)
         b = algo_bytes(N, K, M)
         per_n[N] = {"us_per_call": round(us, 3), "gbs": round(b / us / 1e3, 1),

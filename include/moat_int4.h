@@ -103,7 +103,9 @@ typedef struct moat_int4_gemm_options {
   int32_t finish; /* split-K hand-off, MOAT_FINISH_*; 0 automatic */
   int32_t front;  /* weight loads, MOAT_FRONT_*; 0 automatic */
   int32_t group;  /* record-stream kernel: adjacent 256-column tiles per workgroup, 1, 2 or 4
-                     (the 4 waves split 4 / group ways over K); 0 automatic */
+                     (the workgroup's waves split waves / group ways over K); 0 automatic */
+  int32_t waves;  /* record-stream kernel: waves per workgroup, 4 or 8 (8 applies for n <= 16,
+                     larger n runs on 4); 0 automatic */
 } moat_int4_gemm_options;
 
 #define MOAT_FINISH_AUTO 0

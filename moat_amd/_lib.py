@@ -31,7 +31,8 @@ class GemmOptions(ctypes.Structure):
     """``moat_int4_gemm_options``: zero fields mean automatic."""
     _fields_ = [("algo", ctypes.c_int32), ("splits", ctypes.c_int32),
                 ("batch", ctypes.c_int32), ("finish", ctypes.c_int32), ("front", ctypes.c_int32),
-                ("group", ctypes.c_int32)]
+                ("group", ctypes.c_int32),
+                ("waves", ctypes.c_int32)]
 
 _P = ctypes.c_void_p
 _I32 = ctypes.c_int32

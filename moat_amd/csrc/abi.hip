@@ -27,11 +27,11 @@ int gemm_rounds(int k);
 bool gemm_records_eligible(int k, int m);
 int gemm_records_tiles(int m);
 int gemm_records_groups(int m, int group_tiles);
-size_t gemm_records_lds(int n, int depth, int group_tiles);
+size_t gemm_records_lds(int n, int depth, int group_tiles, int waves);
 bool gemm_records_shares_tiles(int k, int m, int group_tiles, int wgs);
 hipError_t launch_gemm(int algo, const uint16_t* x, const uint8_t* sb, float* y, int n, int k, int m, int splits,
-                       int batch, int finish, int front, int group, float* partials, uint32_t* counters,
-                       hipStream_t stream);
+                       int batch, int finish, int front, int group, int waves, float* partials,
+                       uint32_t* counters, hipStream_t stream);
 }  // namespace moat
 
 namespace {
@@ -55,6 +55,7 @@ struct GemmPlan {
   int finish;  // kernel-side FinishMode: 0 device atomics, 1 fences, 2 second kernel
   int front;   // kernel-side front end: 0 direct, 1 LDS DMA, 2 vector loads + LDS, 3 record stream
   int group;   // record stream: 256-column tiles per workgroup
+  int waves;   // record stream: waves per workgroup (4 or 8)
   int64_t counter_bytes;
   int64_t workspace_bytes;
 };
@@ -75,6 +76,7 @@ bool options_ok(const moat_int4_gemm_options* o, int32_t n) {
   if (o->finish < 0 || o->finish > 3) return false;
   if (o->front < 0 || o->front > 4) return false;
   if (o->group != 0 && o->group != 1 && o->group != 2 && o->group != 4) return false;
+  if (o->waves != 0 && o->waves != 4 && o->waves != 8) return false;
   if (o->algo == MOAT_GEMM_DOT2 && n > kMaxDot2N) return false;
   return true;
 }
@@ -85,7 +87,7 @@ bool options_ok(const moat_int4_gemm_options* o, int32_t n) {
 // splits * N * M * 8 bytes against 0.5625 * K * M bytes of weights; it is kept
 // below a quarter of the weight stream.
 GemmPlan plan_gemm(int32_t n, int32_t k, int32_t m, const moat_int4_gemm_options* o) {
-  moat_int4_gemm_options opt = {0, 0, 0, 0, 0, 0};
+  moat_int4_gemm_options opt = {0, 0, 0, 0, 0, 0, 0};
   if (o) opt = *o;
   GemmPlan p;
   const bool records_ok = moat::gemm_records_eligible(k, m);
@@ -104,18 +106,23 @@ GemmPlan plan_gemm(int32_t n, int32_t k, int32_t m, const moat_int4_gemm_options
     // (2 per CU), and a K split whose fp32 partials stay well below the
     // weight stream.
     const int group = opt.group ? opt.group : 1;
+    // 8 waves per workgroup only up to 16 rows (the accumulators of 32 rows
+    // need more registers than 8 waves leave a lane)
+    const int waves = (opt.waves && n <= 16) ? opt.waves : 4;
     const int groups = moat::gemm_records_groups(m, group);
     const int64_t tiles_r = moat::gemm_records_tiles(m);
-    const int depth = opt.batch ? opt.batch : (n <= 16 ? 3 : 2);  // ring depth (LDS: 4 waves x depth x 7 or 8 KB)
+    // ring depth (LDS: waves x depth x 7 or 8 KB; the launch clamps it to the LDS)
+    const int depth = opt.batch ? opt.batch : (waves == 8 ? 2 : (n <= 16 ? 3 : 2));
     int64_t splits;
     if (opt.splits > 0) {
       splits = opt.splits;
     } else {
-      splits = (tiles_r * rounds / 8 + groups / 2) / groups;  // ~2 rounds per wave
+      // about 8 rounds per workgroup: 2 per wave with 4 waves, 1 with 8
+      splits = (tiles_r * rounds / 8 + groups / 2) / groups;
       if (splits > 8) splits = 8;  // beyond 8 the hand-off costs more than the shorter loop saves
       // no more workgroups than the 256 CUs hold at once (a second wave of
       // workgroups would double the time)
-      const int64_t per_cu = (int64_t)(160 * 1024) / (int64_t)moat::gemm_records_lds(n, depth, group);
+      const int64_t per_cu = (int64_t)(160 * 1024) / (int64_t)moat::gemm_records_lds(n, depth, group, waves);
       const int64_t resident = 256 * (per_cu > 0 ? per_cu : 1);
       const int64_t cap_wgs = resident / groups > 0 ? resident / groups : 1;
       if (splits > cap_wgs) splits = cap_wgs;
@@ -135,6 +142,7 @@ GemmPlan plan_gemm(int32_t n, int32_t k, int32_t m, const moat_int4_gemm_options
     if (wgs > items) wgs = items;
     p.splits = (int)wgs;
     p.group = group;
+    p.waves = waves;
     p.batch = depth;
     // shared tile groups: summed by a fix-up kernel (the default, measured
     // as fast or faster at every N) or, with MOAT_FINISH_DEVICE_ATOMICS or
@@ -171,6 +179,7 @@ GemmPlan plan_gemm(int32_t n, int32_t k, int32_t m, const moat_int4_gemm_options
   p.finish = opt.finish ? opt.finish - 1 : 2;
   p.front = opt.front == MOAT_FRONT_DIRECT ? 0 : (opt.front == MOAT_FRONT_LDS_DMA ? 1 : 2);
   p.group = 1;
+  p.waves = 4;
   if (splits > 1) {
     p.counter_bytes = kCounterBlockBytes;
     p.workspace_bytes = p.counter_bytes + (int64_t)splits * n * m * 4;
@@ -229,7 +238,7 @@ int32_t moat_int4_gemm_ex(const uint16_t* x_f16, const uint8_t* superblocks, flo
     partials = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + p.counter_bytes);
   }
   return status_of(moat::launch_gemm(p.algo, x_f16, superblocks, y_f32, n, k, m, p.splits, p.batch, p.finish,
-                                     p.front, p.group, partials, counters, stream));
+                                     p.front, p.group, p.waves, partials, counters, stream));
 }
 
 int32_t moat_int4_gemm(const uint16_t* x_f16, const uint8_t* superblocks, float* y_f32, int32_t n, int32_t k,

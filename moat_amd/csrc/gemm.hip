@@ -596,31 +596,38 @@ struct RecGeom {
   static constexpr int kLoads = kRecWeightLoads + NR;               // vector-memory instructions per round
 };
 
-// Source offsets (round 0) of a lane's weight slots.  Slot s = 64*i + lane
-// carries chunk c = s % 11 of row s / 11 and lands at byte 16*s of the stage,
-// so row t starts at byte 176*t.  Slots that carry nothing the tile needs
-// (chunk 9 of an aligned row, chunk 10, the slots past row 31, groups past M
-// in the last tile) re-load the row's first header chunk: every round issues
-// the same instructions, which keeps the vmcnt arithmetic exact, and every
-// address stays inside the stream.
+// Source offsets of a lane's weight slots, relative to the first record the
+// tile touches in the round (byte 144 * tile of the round): slot s = 64*i +
+// lane carries chunk c = s % 11 of row s / 11 and lands at byte 16*s of the
+// stage, so row t starts at byte 176*t.  Apart from the tile's base, which is
+// wave-uniform and travels in scalar registers, the offsets depend on the lane
+// and on M only; a 128-column last tile (M % 256 == 128) has its own set.
+// Slots that carry nothing the tile needs (chunk 9 of an aligned row, chunk 10,
+// the slots past row 31, groups 4-7 in a 128-column tile) re-load the row's
+// first header chunk: every round issues the same instructions, which keeps
+// the vmcnt arithmetic exact, and every address stays inside the stream.
 struct RecSlots {
-  uint32_t off[kRecWeightLoads];
+  uint32_t full[kRecWeightLoads];  // 256-column tile
+  uint32_t half[kRecWeightLoads];  // 128-column last tile
 };
 
-__device__ __forceinline__ void rec_slots(RecSlots& s, int lane, int tile, int m, int groups) {
+__device__ __forceinline__ void rec_slots(RecSlots& s, int lane, int m) {
+  const uint32_t halves_per_row = (uint32_t)m >> 7;  // 128-column halves of a row
 #pragma unroll
   for (int i = 0; i < kRecWeightLoads; ++i) {
     const int slot = 64 * i + lane;
     const int row = min(slot / kRecSlotsPerRow, kRoundRows - 1);
     const int c = slot < kRoundRows * kRecSlotsPerRow ? slot % kRecSlotsPerRow : kRecSlotsPerRow - 1;
-    const uint32_t flat = (uint32_t)row * (uint32_t)m + (uint32_t)(kRecCols * tile);
-    const uint32_t head = (flat >> 8) * kSbBytes;
-    // record-aligned row: header, then payload chunk c-1 at 16*c
-    const uint32_t al = (c >= 1 && c <= 8 && c - 1 < groups) ? head + 16 * c : head;
-    // shifted row: header of s, chunks 4-7 of s, header of s+1, chunks 0-3 of s+1
-    const bool pay_sh = (c >= 1 && c <= 4) ? (c - 1 < groups) : (c >= 6 && c - 2 < groups);
-    const uint32_t sh = pay_sh ? head + 64 + 16 * c : ((c == 5 && groups > 4) ? head + kSbBytes : head);
-    s.off[i] = ((flat >> 7) & 1) ? sh : al;
+    const uint32_t halves = (uint32_t)row * halves_per_row;  // row start, in 128-column units
+    const uint32_t head = (halves >> 1) * kSbBytes;          // the record the row starts in
+    const bool shifted = halves & 1;                         // ... half-way in
+    // aligned row: header, then payload chunk c-1 at 16*c (c = 1..8).
+    // shifted row: header of s, chunks 4-7 of s (c = 1..4), header of s+1
+    // (c = 5) and chunks 0-3 of s+1 (c = 6..9): one window from byte 80.
+    const uint32_t pay = 16 * c + (shifted ? 64 : 0);
+    const int last_full = shifted ? 9 : 8;
+    s.full[i] = head + ((c >= 1 && c <= last_full) ? pay : 0u);
+    s.half[i] = head + ((c >= 1 && c <= 4) ? pay : 0u);
   }
 }
 
@@ -633,25 +640,25 @@ __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("" ::: "memory");
 }
 
-// One global_load_lds_dwordx4: lane l's 16 bytes at `src` land at LDS byte
-// lds_base + 16*l.  Written as inline assembly so that the compiler, which
-// cannot tell the ring's stages apart, does not guard every later LDS read
-// with a wait for all of these copies; the explicit vmcnt waits above are the
-// only ordering the ring needs.  (s_nop: one wait state between writing M0
-// and the instruction that reads it.)
-__device__ __forceinline__ void lds_dma16(const void* src, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(src), "s"(lds_base)
-               : "memory", "m0");
+// One global_load_lds_dwordx4: lane l's 16 bytes at base + off (base in
+// scalar registers, a 32-bit per-lane offset) land at LDS byte lds_base +
+// 16*l.  Written as inline assembly so that the compiler, which cannot tell
+// the ring's stages apart, does not guard every later LDS read with a wait for
+// all of these copies; the explicit vmcnt waits above are the only ordering
+// the ring needs.  (s_nop: one wait state between writing M0 and the
+// instruction that reads it.)
+__device__ __forceinline__ void lds_dma16(const void* base, uint32_t off, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(off), "s"(base),
+               "s"(lds_base) : "memory", "m0");
 }
 
 template <int NR>
-__device__ __forceinline__ void rec_issue(const RecSlots& s, const uint8_t* __restrict__ wround,
-                                          const uint8_t* __restrict__ xround, const uint32_t (&xoff)[NR],
-                                          uint32_t stage) {
+__device__ __forceinline__ void rec_issue(const uint32_t (&woff)[kRecWeightLoads], const uint8_t* wround,
+                                          const uint8_t* xround, const uint32_t (&xoff)[NR], uint32_t stage) {
 #pragma unroll
-  for (int i = 0; i < kRecWeightLoads; ++i) lds_dma16(wround + s.off[i], stage + 1024 * i);
+  for (int i = 0; i < kRecWeightLoads; ++i) lds_dma16(wround, woff[i], stage + 1024 * i);
 #pragma unroll
-  for (int nt = 0; nt < NR; ++nt) lds_dma16(xround + xoff[nt], stage + kRecWeightBytes + 1024 * nt);
+  for (int nt = 0; nt < NR; ++nt) lds_dma16(xround, xoff[nt], stage + kRecWeightBytes + 1024 * nt);
 }
 
 // Per-lane LDS read offsets inside a stage: payload (8 bytes = the lane's 16
@@ -769,12 +776,12 @@ __device__ __forceinline__ void load8_sc1(float4_t (&t)[8], const float* const (
 // (slot s of tile tl at red + (tl * nslots + s) * per_slot) and goes to Y
 // (part == nullptr) or to the partial slot part + tl * per_slot.  The whole
 // workgroup stores, one 4-column quad per thread and step.
-template <int kC>
+template <int kC, int kW>
 __device__ __forceinline__ void rec_store(const GemmParams& P, const float* red, int per_slot, int nslots, int tg,
                                           float* part, bool coherent) {
   const int total = kC * P.n * 64;
-  for (int idx = threadIdx.x; idx < total; idx += kThreads) {
-    const int tl = idx / (P.n * 64);
+  for (int idx = threadIdx.x; idx < total; idx += kW * 64) {
+    const int tl = kC == 1 ? 0 : idx / (P.n * 64);
     const int w = idx - tl * P.n * 64;
     const int row = w >> 6, qd = w & 63;
     const int tile = tg * kC + tl;
@@ -782,7 +789,7 @@ __device__ __forceinline__ void rec_store(const GemmParams& P, const float* red,
     if (m0 + 4 * qd >= P.m) continue;
     const float* base = red + tl * nslots * per_slot + red_pos(row, qd >> 2, qd & 3);
     float4_t v = *reinterpret_cast<const float4_t*>(base);
-    if (nslots > 1) v += *reinterpret_cast<const float4_t*>(base + per_slot);
+    for (int sl = 1; sl < nslots; ++sl) v += *reinterpret_cast<const float4_t*>(base + sl * per_slot);
     if (part) {
       float* pp = part + tl * per_slot + row * kRecCols + 4 * qd;
       if (coherent) store_sc1(pp, v);
@@ -804,7 +811,7 @@ __device__ __forceinline__ void rec_store(const GemmParams& P, const float* red,
 // counts the contributors; the last one adds every contributor's partials in
 // workgroup order (sc1 loads, eight in flight), writes Y and clears the
 // counter for the next call.
-template <int kC>
+template <int kC, int kW>
 __device__ __forceinline__ void rec_handoff(const GemmParams& P, int tg) {
   __shared__ int s_last;
   asm volatile("s_waitcnt vmcnt(0)" : : : "memory");  // this thread's partial stores are complete
@@ -819,8 +826,8 @@ __device__ __forceinline__ void rec_handoff(const GemmParams& P, int tg) {
   if (!s_last) return;
   const int per_slot = P.n * kRecCols;
   const int total = kC * P.n * 64;
-  for (int idx = threadIdx.x; idx < total; idx += kThreads) {
-    const int tl = idx / (P.n * 64);
+  for (int idx = threadIdx.x; idx < total; idx += kW * 64) {
+    const int tl = kC == 1 ? 0 : idx / (P.n * 64);
     const int w = idx - tl * P.n * 64;
     const int row = w >> 6, qd = w & 63;
     const int m0 = (tg * kC + tl) * kRecCols;
@@ -853,16 +860,16 @@ __device__ __forceinline__ void rec_handoff(const GemmParams& P, int tg) {
   if (threadIdx.x == 0) __hip_atomic_store(&P.counters[tg], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int NR, int kDepth, int kC>
-__global__ void __launch_bounds__(kThreads) int4_gemm_records_kernel(GemmParams P) {
+template <int NR, int kDepth, int kC, int kW>
+__global__ void __launch_bounds__(kW * 64) int4_gemm_records_kernel(GemmParams P) {
   using G = RecGeom<NR>;
-  constexpr int kShare = kWaves / kC;  // waves per tile
+  constexpr int kShare = kW / kC;  // waves per tile
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   // fetch every argument now, in one batch of scalar loads, rather than at
   // first use (each late load is another serial trip to memory)
   asm volatile("" : : "s"(P.x), "s"(P.sb), "s"(P.y), "s"(P.partials), "s"(P.n), "s"(P.k), "s"(P.m),
                "s"(P.rounds), "s"(P.shift), "s"(P.y_vec), "s"(P.items_base), "s"(P.items_rem), "s"(P.tiles),
-               "s"(P.counters), "s"(P.finish));
+               "s"(P.counters), "s"(P.finish), "s"(P.splits));
   const int lane = threadIdx.x & 63;
   // wave index as a scalar: the round loop below is then uniform control flow
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -895,17 +902,22 @@ __global__ void __launch_bounds__(kThreads) int4_gemm_records_kernel(GemmParams 
   }
   // workgroup ids are dealt round-robin to the 8 XCDs: give each XCD one
   // contiguous run of ranges, so that the tiles it shares meet in its L2
-  const int nwg = gridDim.x, b = blockIdx.x, per = nwg / kXcds;
+  // (the workgroup count is P.splits: the grid size would be one more serial
+  // load from the dispatch's hidden arguments)
+  const int nwg = P.splits, b = blockIdx.x, per = nwg / kXcds;
   const int p = b < per * kXcds ? (b % kXcds) * per + b / kXcds : b;
   int lo, hi;
   streamk_range(P, p, lo, hi);
 
   const uint64_t round_bytes = (uint64_t)18 * (uint64_t)P.m;
+  RecSlots slots;
+  rec_slots(slots, lane, P.m);
   uint8_t* ring = smem + wave * kDepth * G::kStageBytes;
   const uint32_t ring_lds = (uint32_t)(uintptr_t)(lds_ptr_t)ring;  // LDS byte address (wave-uniform)
   float* red = reinterpret_cast<float*>(smem);
   const int per_slot = P.n * kRecCols;
-  constexpr int kSlots = kShare == 4 ? 2 : 1;  // reduction slots per tile
+  constexpr int kHalf = kShare >= 2 ? kShare / 2 : 1;
+  constexpr int kSlots = kHalf;  // reduction slots per tile
 
   for (int seg_lo = lo; seg_lo < hi;) {
     const int tg = seg_lo / P.rounds;
@@ -916,8 +928,10 @@ __global__ void __launch_bounds__(kThreads) int4_gemm_records_kernel(GemmParams 
     const bool has_tile = tile < P.tiles;  // the last group may be short
     const int groups = has_tile ? min(8, (P.m - kRecCols * tile) >> 5) : 0;  // 4 or 8 (M % 128 == 0)
     const uint32_t smask = g < groups ? 0xFFFFFFFFu : 0u;
-    RecSlots slots;
-    rec_slots(slots, lane, has_tile ? tile : 0, P.m, has_tile ? groups : 8);
+    uint32_t woff[kRecWeightLoads];
+#pragma unroll
+    for (int i = 0; i < kRecWeightLoads; ++i) woff[i] = groups < 8 ? slots.half[i] : slots.full[i];
+    const uint8_t* wtile = P.sb + (uint64_t)kSbBytes * (has_tile ? tile : 0);
 
     RecAcc<NR> acc;
 #pragma unroll
@@ -929,7 +943,7 @@ __global__ void __launch_bounds__(kThreads) int4_gemm_records_kernel(GemmParams 
     const int cnt = (has_tile && first < r1) ? (r1 - first + kShare - 1) / kShare : 0;
     auto issue = [&](int i) {
       const int r = first + kShare * i;
-      rec_issue<NR>(slots, P.sb + (uint64_t)r * round_bytes, reinterpret_cast<const uint8_t*>(P.x) + 64 * r, xoff,
+      rec_issue<NR>(woff, wtile + (uint64_t)r * round_bytes, reinterpret_cast<const uint8_t*>(P.x) + 64 * r, xoff,
                     __builtin_amdgcn_readfirstlane(ring_lds + (i % kDepth) * G::kStageBytes));
     };
 #pragma unroll
@@ -951,18 +965,19 @@ __global__ void __launch_bounds__(kThreads) int4_gemm_records_kernel(GemmParams 
     }
     __syncthreads();  // the ring is reused for the reduction
 
-    // Waves of one tile add up through LDS: with 4 waves per tile, waves
-    // with kpart 2, 3 store into the tile's two slots and kpart 0, 1 add
-    // theirs; with 2, kpart 1 stores and kpart 0 adds; with 1 the wave stores.
-    // Lane (q, j) holds D[16*nt + 4q + v][16j + c]; 4 columns per access.
+    // Waves of one tile add up through LDS: the upper half of its waves
+    // (kpart >= kShare / 2) store into the tile's kShare / 2 slots, the lower
+    // half add theirs, and the store below sums the slots; a single wave
+    // per tile just stores.  Lane (q, j) holds D[16*nt + 4q + v][16j + c];
+    // 4 columns per access.
     float* tred = red + tl * kSlots * per_slot;
     constexpr int kPhases = kShare > 1 ? 2 : 1;
 #pragma unroll
     for (int phase = 0; phase < kPhases; ++phase) {
-      const bool active = kShare == 1 ? true : (kShare == 2 ? (kpart == 1 - phase) : ((kpart >> 1) == 1 - phase));
+      const bool active = kShare == 1 ? true : (phase == 0 ? kpart >= kHalf : kpart < kHalf);
       const bool add = kShare > 1 && phase == 1;
       if (active) {
-        float* slot = tred + (kShare == 4 ? (kpart & 1) : 0) * per_slot;
+        float* slot = tred + (kpart % kHalf) * per_slot;
 #pragma unroll
         for (int nt = 0; nt < NR; ++nt)
 #pragma unroll
@@ -985,9 +1000,9 @@ __global__ void __launch_bounds__(kThreads) int4_gemm_records_kernel(GemmParams 
     const bool whole = r0 == 0 && r1 == P.rounds;
     const int pslot = 2 * p + (seg_lo == lo ? 0 : 1);
     const bool in_kernel = P.finish != kFinishSecondKernel;
-    rec_store<kC>(P, red, per_slot, kSlots, tg, whole ? nullptr : P.partials + (int64_t)pslot * kC * per_slot,
-                  in_kernel);
-    if (!whole && in_kernel) rec_handoff<kC>(P, tg);
+    rec_store<kC, kW>(P, red, per_slot, kSlots, tg, whole ? nullptr : P.partials + (int64_t)pslot * kC * per_slot,
+                      in_kernel);
+    if (!whole && in_kernel) rec_handoff<kC, kW>(P, tg);
     __syncthreads();  // LDS is the next segment's ring
     seg_lo = seg_hi;
   }
@@ -1098,45 +1113,59 @@ static hipError_t launch_front(const GemmParams& P, int algo, int batch, hipStre
   return launch_gemm_variant<1, kFront>(P, algo, stream);
 }
 
-template <int NR, int kDepth, int kC>
+// Reduction slots of one tile: half the waves that share it (one at least).
+constexpr int rec_slots_per_tile(int waves, int group_tiles) {
+  return waves / group_tiles >= 2 ? waves / group_tiles / 2 : 1;
+}
+
+template <int NR, int kDepth, int kC, int kW>
 static hipError_t launch_records_one(const GemmParams& P, int wgs, hipStream_t stream) {
-  constexpr int kShare = kWaves / kC;
-  const size_t ring = (size_t)kWaves * kDepth * RecGeom<NR>::kStageBytes;
-  const size_t red = (size_t)kC * (kShare == 4 ? 2 : 1) * P.n * kRecCols * sizeof(float);
+  const size_t ring = (size_t)kW * kDepth * RecGeom<NR>::kStageBytes;
+  const size_t red = (size_t)kC * rec_slots_per_tile(kW, kC) * P.n * kRecCols * sizeof(float);
   if (ring > kMaxDynamicLds || red > kMaxDynamicLds) return hipErrorInvalidValue;  // never launch past the LDS
-  hipLaunchKernelGGL((int4_gemm_records_kernel<NR, kDepth, kC>), dim3(wgs), dim3(kThreads), ring > red ? ring : red,
-                     stream, P);
+  hipLaunchKernelGGL((int4_gemm_records_kernel<NR, kDepth, kC, kW>), dim3(wgs), dim3(kW * 64),
+                     ring > red ? ring : red, stream, P);
   return hipGetLastError();
 }
 
-template <int NR, int kC>
+template <int NR, int kC, int kW>
 static hipError_t launch_records_depth(const GemmParams& P, int wgs, int depth, hipStream_t stream) {
-  // the ring must fit: clamp the depth (4 waves x depth stages)
-  const int max_depth = (int)(kMaxDynamicLds / ((size_t)kWaves * RecGeom<NR>::kStageBytes));
+  // the ring must fit: clamp the depth (kW waves x depth stages)
+  const int max_depth = (int)(kMaxDynamicLds / ((size_t)kW * RecGeom<NR>::kStageBytes));
   if (depth > max_depth) depth = max_depth;
-  if (depth >= 5) return launch_records_one<NR, 5, kC>(P, wgs, stream);
-  if (depth == 4) return launch_records_one<NR, 4, kC>(P, wgs, stream);
-  if (depth == 3) return launch_records_one<NR, 3, kC>(P, wgs, stream);
-  if (depth == 2) return launch_records_one<NR, 2, kC>(P, wgs, stream);
-  return launch_records_one<NR, 1, kC>(P, wgs, stream);
+  if (depth >= 5) return launch_records_one<NR, 5, kC, kW>(P, wgs, stream);
+  if (depth == 4) return launch_records_one<NR, 4, kC, kW>(P, wgs, stream);
+  if (depth == 3) return launch_records_one<NR, 3, kC, kW>(P, wgs, stream);
+  if (depth == 2) return launch_records_one<NR, 2, kC, kW>(P, wgs, stream);
+  return launch_records_one<NR, 1, kC, kW>(P, wgs, stream);
 }
 
+template <int NR, int kW>
+static hipError_t launch_records_group(const GemmParams& P, int wgs, int depth, int group_tiles, hipStream_t stream) {
+  if (group_tiles == 4) return launch_records_depth<NR, 4, kW>(P, wgs, depth, stream);
+  if (group_tiles == 2) return launch_records_depth<NR, 2, kW>(P, wgs, depth, stream);
+  return launch_records_depth<NR, 1, kW>(P, wgs, depth, stream);
+}
+
+// 8 waves hold at most 256 registers per lane, too few for the accumulators
+// of 32 rows: those run on 4 waves (the plan never asks otherwise)
 template <int NR>
-static hipError_t launch_records(const GemmParams& P, int wgs, int depth, int group_tiles, hipStream_t stream) {
-  if (group_tiles == 4) return launch_records_depth<NR, 4>(P, wgs, depth, stream);
-  if (group_tiles == 2) return launch_records_depth<NR, 2>(P, wgs, depth, stream);
-  return launch_records_depth<NR, 1>(P, wgs, depth, stream);
+static hipError_t launch_records(const GemmParams& P, int wgs, int depth, int group_tiles, int waves,
+                                 hipStream_t stream) {
+  if (NR == 1 && waves == 8) return launch_records_group<1, 8>(P, wgs, depth, group_tiles, stream);
+  if (waves != 4) return hipErrorInvalidValue;
+  return launch_records_group<NR, 4>(P, wgs, depth, group_tiles, stream);
 }
 
 bool gemm_records_eligible(int k, int m) { return (m % 128) == 0 && (k % kRoundRows) == 0; }
 
 // Dynamic LDS of one record-stream workgroup (after the depth clamp).
-size_t gemm_records_lds(int n, int depth, int group_tiles) {
+size_t gemm_records_lds(int n, int depth, int group_tiles, int waves) {
   const size_t stage = n <= 16 ? RecGeom<1>::kStageBytes : RecGeom<2>::kStageBytes;
-  const int max_depth = (int)(kMaxDynamicLds / (kWaves * stage));
+  const int max_depth = (int)(kMaxDynamicLds / (waves * stage));
   if (depth > max_depth) depth = max_depth;
-  const size_t ring = (size_t)kWaves * depth * stage;
-  const size_t red = (size_t)group_tiles * (group_tiles == 1 ? 2 : 1) * n * kRecCols * sizeof(float);
+  const size_t ring = (size_t)waves * depth * stage;
+  const size_t red = (size_t)group_tiles * rec_slots_per_tile(waves, group_tiles) * n * kRecCols * sizeof(float);
   return ring > red ? ring : red;
 }
 int gemm_records_tiles(int m) { return (m + kRecCols - 1) / kRecCols; }
@@ -1152,7 +1181,7 @@ bool gemm_records_shares_tiles(int k, int m, int group_tiles, int wgs) {
 }
 
 hipError_t launch_gemm(int algo, const uint16_t* x, const uint8_t* sb, float* y, int n, int k, int m, int splits,
-                       int batch, int finish, int front, int group, float* partials, uint32_t* counters,
+                       int batch, int finish, int front, int group, int waves, float* partials, uint32_t* counters,
                        hipStream_t stream) {
   GemmParams P;
   P.x = x; P.sb = sb; P.y = y; P.partials = partials; P.counters = counters;
@@ -1177,8 +1206,8 @@ hipError_t launch_gemm(int algo, const uint16_t* x, const uint8_t* sb, float* y,
       P.items_base = items / wgs;
       P.items_rem = items % wgs;
       P.y_vec = ((reinterpret_cast<uintptr_t>(y) & 15) == 0) ? 1 : 0;
-      e = P.n <= 16 ? launch_records<1>(P, wgs, batch, group_tiles, stream)
-                    : launch_records<2>(P, wgs, batch, group_tiles, stream);
+      e = P.n <= 16 ? launch_records<1>(P, wgs, batch, group_tiles, waves, stream)
+                    : launch_records<2>(P, wgs, batch, group_tiles, waves, stream);
       if (e != hipSuccess || !gemm_records_shares_tiles(k, m, group_tiles, wgs) || finish != kFinishSecondKernel)
         return e;
       const int quads = P.tiles * P.n * 64;

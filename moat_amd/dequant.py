@@ -280,28 +280,29 @@ def quantize_to_superblocks(weights, scale_rule: str = "f32"):
 
 def _gemm_into(x: torch.Tensor, blob: torch.Tensor, y: torch.Tensor, K: int, M: int,
                algo: int = _lib.GEMM_AUTO, splits: int = 0, batch: int = 0, finish: int = 0, front: int = 0,
-               group: int = 0) -> None:
+               group: int = 0, waves: int = 0) -> None:
     lib = _lib.load()
     n = x.shape[0]
-    opt = _lib.GemmOptions(algo, splits, batch, finish, front, group)
+    opt = _lib.GemmOptions(algo, splits, batch, finish, front, group, waves)
     ws_bytes = lib.moat_int4_gemm_ex_workspace_size(n, K, M, ctypes.byref(opt))
     if ws_bytes < 0:
         raise ValueError(f"unsupported GEMM configuration N={n} K={K} M={M} algo={algo} splits={splits} "
-                         f"batch={batch} finish={finish} front={front} group={group}")
+                         f"batch={batch} finish={finish} front={front} group={group} waves={waves}")
     ws = D.workspaces.get(ws_bytes)
     _lib.check(lib.moat_int4_gemm_ex(D.ptr(x), D.ptr(blob), D.ptr(y), n, K, M, ctypes.byref(opt),
                                      D.ptr(ws), ws_bytes, D.stream()), "batched_int4_matmul")
 
 
 def batched_int4_matmul(x, superblocks, K: int, M: int, out=None, *, algo: int = _lib.GEMM_AUTO,
-                        splits: int = 0, batch: int = 0, finish: int = 0, front: int = 0, group: int = 0):
+                        splits: int = 0, batch: int = 0, finish: int = 0, front: int = 0, group: int = 0,
+                        waves: int = 0):
     """``Y[N, M] = f32(X[N, K]) @ f32(deq(W)[K, M])`` with W the 144-byte stream
     of a row-major K x M matrix; fp32 out.  Equal (to float32 summation order)
     to decoding with :func:`unpack_superblock_weights` and a float32 matmul.
     ValueError unless ``M % 32 == 0`` and ``K*M % 256 == 0``.  N above 32 is
     processed in slices of 32 rows.  ``algo``/``splits``/``batch``/``finish``/
-    ``front``/``group`` override the launch choices of ``moat_int4_gemm_options``
-    (0 = automatic)."""
+    ``front``/``group``/``waves`` override the launch choices of
+    ``moat_int4_gemm_options`` (0 = automatic)."""
     want_t = D.is_tensor(x)
     K, M = int(K), int(M)
     if K < 1 or M < 32 or M % 32 != 0 or (K * M) % SUPERBLOCK_ELEMS != 0:
@@ -325,7 +326,7 @@ def batched_int4_matmul(x, superblocks, K: int, M: int, out=None, *, algo: int =
         y = torch.empty((N, M), dtype=torch.float32, device=xs.device)
     for r0 in range(0, N, MAX_BATCH_PER_CALL):
         r1 = min(N, r0 + MAX_BATCH_PER_CALL)
-        _gemm_into(xs[r0:r1], blob, y[r0:r1], K, M, algo, splits, batch, finish, front, group)
+        _gemm_into(xs[r0:r1], blob, y[r0:r1], K, M, algo, splits, batch, finish, front, group, waves)
     if out is not None and not D.is_tensor(out):
         np.copyto(out, D.to_host(y))
         return out

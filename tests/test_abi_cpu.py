@@ -79,7 +79,9 @@ def test_gemm_rejects_null_and_misaligned(lib):
         assert lib.moat_int4_gemm_ex(FAKE, FAKE, FAKE, 9, 256, 256, ctypes.byref(opt), None, 0, None) == _lib.MOAT_ERR_INVALID
     for opt in (_lib.GemmOptions(7, 1, 0, 0), _lib.GemmOptions(0, 1, 6, 0), _lib.GemmOptions(0, 1, -1, 0),
                 _lib.GemmOptions(0, 1, 0, 4), _lib.GemmOptions(0, 1, 0, 0, 5), _lib.GemmOptions(0, -1, 0, 0),
-                _lib.GemmOptions(0, 1, 0, 0, 4, 3), _lib.GemmOptions(0, 1, 0, 0, 4, 8)):
+                _lib.GemmOptions(0, 1, 0, 0, 4, 3), _lib.GemmOptions(0, 1, 0, 0, 4, 8),
+                _lib.GemmOptions(0, 1, 0, 0, 4, 1, 6), _lib.GemmOptions(0, 1, 0, 0, 4, 1, 16),
+                _lib.GemmOptions(0, 1, 0, 0, 4, 1, -4)):
         assert lib.moat_int4_gemm_ex(FAKE, FAKE, FAKE, 1, 256, 256, ctypes.byref(opt), None, 0, None) == _lib.MOAT_ERR_INVALID
         assert lib.moat_int4_gemm_ex_workspace_size(1, 256, 256, ctypes.byref(opt)) == -1
 
@@ -99,6 +101,10 @@ def test_gemm_workspace_contract(lib):
     assert lib.moat_int4_gemm_ex_workspace_size(4, 2048, 5504, ctypes.byref(rec4)) == 64 * 1024 + 2 * 6 * 8 * 4 * 4 * 256 * 4
     st = lib.moat_int4_gemm_ex(FAKE, FAKE, FAKE, 4, 2048, 5504, ctypes.byref(rec), None, 0, None)
     assert st == _lib.MOAT_ERR_WORKSPACE
+    # 8 waves per workgroup: the same workgroups and partial slots
+    rec8 = _lib.GemmOptions(_lib.GEMM_MFMA, 8, 0, 0, _lib.FRONT_RECORDS, 1, 8)
+    assert lib.moat_int4_gemm_ex_workspace_size(4, 2048, 5504, ctypes.byref(rec8)) == 64 * 1024 + 2 * 22 * 8 * 4 * 256 * 4
+    assert lib.moat_int4_gemm_ex_workspace_size(32, 2048, 5504, ctypes.byref(rec8)) == 64 * 1024 + 2 * 22 * 8 * 32 * 256 * 4
     # one workgroup per tile: nothing shared, no workspace
     one_rec = _lib.GemmOptions(_lib.GEMM_MFMA, 1, 0, 0, _lib.FRONT_RECORDS, 2)
     assert lib.moat_int4_gemm_ex_workspace_size(4, 2048, 5504, ctypes.byref(one_rec)) == 0

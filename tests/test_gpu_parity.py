@@ -155,8 +155,9 @@ def test_gemm_record_stream_kernel(K, M):
     """The record-stream kernel (256-column tiles of whole records; rows that
     start half-way into a record when M % 256 == 128; a 128-column last tile;
     a short last tile group; waves with no round when K is short) at every
-    tile-group size, ring depth, stream-K split and hand-off (last workgroup
-    in the kernel, or the fix-up kernel)."""
+    tile-group size, workgroup size (4 or 8 waves), ring depth (deeper
+    than the LDS holds: clamped), stream-K split and hand-off (last
+    workgroup in the kernel, or the fix-up kernel)."""
     from moat_amd.dequant import batched_int4_matmul
     L = _lib()
     w = O.synthetic_weights(K, M, 0.03, 11 + K + M)
@@ -168,16 +169,17 @@ def test_gemm_record_stream_kernel(K, M):
         x = _x(N, K, 21 + N)
         yref = x.astype(np.float32) @ wdq
         xd = torch.from_numpy(x).cuda()
-        for group in (1, 2, 4):
-            for depth in (1, 2, 3, 5):
-                for splits in sorted({1, 2, min(5, rounds), min(16, rounds)}):
-                    for finish in (L.FINISH_AUTO, L.FINISH_SECOND_KERNEL):
-                        say(f"case: records K={K} M={M} N={N} group={group} depth={depth} splits={splits} "
-                            f"finish={finish}")
-                        y = batched_int4_matmul(xd, blob_d, K, M, algo=L.GEMM_MFMA, splits=splits, batch=depth,
-                                                finish=finish, front=L.FRONT_RECORDS, group=group)
-                        e = rel_err(y.cpu().numpy(), yref)
-                        assert e <= TOL, (K, M, N, group, depth, splits, finish, e)
+        for waves, depths in ((4, (1, 2, 3, 5)), (8, (1, 2, 5))):
+            for group in (1, 2, 4):
+                for depth in depths:
+                    for splits in sorted({1, 2, min(5, rounds), min(16, rounds)}):
+                        for finish in (L.FINISH_AUTO, L.FINISH_SECOND_KERNEL):
+                            say(f"case: records K={K} M={M} N={N} waves={waves} group={group} depth={depth} "
+                                f"splits={splits} finish={finish}")
+                            y = batched_int4_matmul(xd, blob_d, K, M, algo=L.GEMM_MFMA, splits=splits, batch=depth,
+                                                    finish=finish, front=L.FRONT_RECORDS, group=group, waves=waves)
+                            e = rel_err(y.cpu().numpy(), yref)
+                            assert e <= TOL, (K, M, N, waves, group, depth, splits, finish, e)
 
 
 def test_gemm_workspace_shared_between_kernels():

@@ -24,26 +24,21 @@ WEIGHT_LOADS = 6
 
 
 def rec_slots(lane, tile, m, groups):
+    """Absolute source offsets (round 0) of a lane's weight slots: the tile's
+    base 144*tile (scalar in the kernel) plus the lane's offset from the full
+    or the 128-column set (``rec_slots``: ``full`` / ``half``)."""
     offs = []
+    halves_per_row = m >> 7
     for i in range(WEIGHT_LOADS):
         slot = 64 * i + lane
-        row, c = divmod(slot, SLOTS_PER_ROW)
-        if row > 31:
-            row, c = 31, SLOTS_PER_ROW - 1
-        flat = row * m + 256 * tile
-        head = (flat >> 8) * 144
-        off = head
-        if ((flat >> 7) & 1) == 0:
-            if 1 <= c <= 8 and c - 1 < groups:
-                off = head + 16 * c
-        else:
-            if 1 <= c <= 4 and c - 1 < groups:
-                off = head + 64 + 16 * c
-            elif c == 5 and groups > 4:
-                off = head + 144
-            elif c >= 6 and c - 2 < groups:
-                off = head + 64 + 16 * c
-        offs.append(off)
+        row = min(slot // SLOTS_PER_ROW, 31)
+        c = slot % SLOTS_PER_ROW if slot < 32 * SLOTS_PER_ROW else SLOTS_PER_ROW - 1
+        halves = row * halves_per_row
+        head = (halves >> 1) * 144
+        shifted = halves & 1
+        pay = 16 * c + (64 if shifted else 0)
+        last = (9 if shifted else 8) if groups == 8 else 4
+        offs.append(144 * tile + head + (pay if 1 <= c <= last else 0))
     return offs
 
 
