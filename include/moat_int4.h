@@ -84,9 +84,10 @@ int32_t moat_int4_dequant(const uint8_t* superblocks, int64_t n_superblocks,
  * workspace: device memory of moat_int4_gemm_workspace_size() bytes (may be
  * NULL when that size is 0): a fixed 64 KB block of split-K counters followed
  * by fp32 partials.  Zero-fill it once before first use (e.g. with
- * moat_int4_workspace_clear); every call leaves the counter block at zero
- * again, so one workspace serves calls of any shape.  Calls that share a
- * workspace must not overlap.  m is limited to 2,097,152.
+ * moat_int4_workspace_clear); every call leaves all of it at zero again (the
+ * record-stream kernel's in-kernel hand-off reads a zero word as "partial not
+ * written yet"), so one workspace serves calls of any shape.  Calls that share
+ * a workspace must not overlap.  m is limited to 2,097,152.
  */
 int64_t moat_int4_gemm_workspace_size(int32_t n, int32_t k, int32_t m);
 int32_t moat_int4_gemm(const uint16_t* x_f16, const uint8_t* superblocks, float* y_f32,
@@ -109,6 +110,14 @@ typedef struct moat_int4_gemm_options {
 } moat_int4_gemm_options;
 
 #define MOAT_FINISH_AUTO 0
+/* General kernel: the last workgroup of a column tile to publish its partial
+ * sums the tile (ATOMICS, FENCES: how the partials are published), or a
+ * second kernel does.  Record-stream kernel: ATOMICS and FENCES both mean the
+ * in-kernel hand-off (the workgroup holding a tile group's last round adds
+ * the others' device-coherent partials), SECOND_KERNEL the fix-up kernel;
+ * automatic: second kernel for the general kernel; for the record-stream
+ * kernel in-kernel while the owner reads at most 64 KB of partials, else the
+ * fix-up kernel. */
 #define MOAT_FINISH_DEVICE_ATOMICS 1 /* partials via device-scope atomic stores/loads, one launch */
 #define MOAT_FINISH_FENCES 2         /* partials via plain stores + agent-scope fences, one launch */
 #define MOAT_FINISH_SECOND_KERNEL 3  /* partials via plain stores, summed by a second kernel */

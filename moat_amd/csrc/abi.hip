@@ -27,7 +27,6 @@ int gemm_rounds(int k);
 bool gemm_records_eligible(int k, int m);
 int gemm_records_tiles(int m);
 int gemm_records_groups(int m, int group_tiles);
-size_t gemm_records_lds(int n, int depth, int group_tiles, int waves);
 bool gemm_records_shares_tiles(int k, int m, int group_tiles, int wgs);
 hipError_t launch_gemm(int algo, const uint16_t* x, const uint8_t* sb, float* y, int n, int k, int m, int splits,
                        int batch, int finish, int front, int group, int waves, float* partials,
@@ -121,9 +120,10 @@ GemmPlan plan_gemm(int32_t n, int32_t k, int32_t m, const moat_int4_gemm_options
       splits = (tiles_r * rounds / 8 + groups / 2) / groups;
       if (splits > 8) splits = 8;  // beyond 8 the hand-off costs more than the shorter loop saves
       // no more workgroups than the 256 CUs hold at once (a second wave of
-      // workgroups would double the time)
-      const int64_t per_cu = (int64_t)(160 * 1024) / (int64_t)moat::gemm_records_lds(n, depth, group, waves);
-      const int64_t resident = 256 * (per_cu > 0 ? per_cu : 1);
+      // workgroups would double the time): one per CU, as the kernel's
+      // registers (over 128 per lane) leave room for one wave per SIMD with 4
+      // waves per workgroup, two with 8
+      const int64_t resident = 256;
       const int64_t cap_wgs = resident / groups > 0 ? resident / groups : 1;
       if (splits > cap_wgs) splits = cap_wgs;
       // above 16 rows the partial sums (N x 256 floats per workgroup) weigh:
@@ -140,14 +140,25 @@ GemmPlan plan_gemm(int32_t n, int32_t k, int32_t m, const moat_int4_gemm_options
     int64_t wgs = (int64_t)groups * splits;
     const int64_t items = (int64_t)groups * rounds;
     if (wgs > items) wgs = items;
+    // the kernel addresses the partials with 32-bit byte offsets
+    const int64_t max_wgs = (int64_t)0xFFFFFFFF / ((int64_t)2 * group * n * 256 * (int64_t)sizeof(float));
+    if (wgs > max_wgs) wgs = max_wgs;
     p.splits = (int)wgs;
     p.group = group;
     p.waves = waves;
     p.batch = depth;
-    // shared tile groups: summed by a fix-up kernel (the default, measured
-    // as fast or faster at every N) or, with MOAT_FINISH_DEVICE_ATOMICS or
-    // MOAT_FINISH_FENCES, by the last contributing workgroup
-    p.finish = (opt.finish == MOAT_FINISH_AUTO || opt.finish == MOAT_FINISH_SECOND_KERNEL) ? 2 : 0;
+    // shared tile groups: summed in the kernel by the workgroup that owns the
+    // group (MOAT_FINISH_DEVICE_ATOMICS or MOAT_FINISH_FENCES) or by a fix-up
+    // kernel (MOAT_FINISH_SECOND_KERNEL).  Automatic: in the kernel while the
+    // owner reads at most 64 KB of partials (n x 1 KB per tile and
+    // contributor), which saves the second launch; beyond that the owner's
+    // one CU is slower than the fix-up kernel spread over many.
+    if (opt.finish == MOAT_FINISH_AUTO) {
+      const int64_t per_group = (wgs + groups - 1) / groups;  // workgroups sharing a tile group
+      p.finish = (int64_t)n * group * (per_group - 1) <= 64 ? 0 : 2;
+    } else {
+      p.finish = opt.finish == MOAT_FINISH_SECOND_KERNEL ? 2 : 0;
+    }
     p.front = 3;
     // the partials follow the fixed counter block, which other calls sharing
     // the workspace rely on staying zero

@@ -381,6 +381,8 @@ __device__ __forceinline__ void finish_tile(const GemmParams& P, float* red, int
     const int64_t o = (int64_t)n * P.m + m0 + c;
     float v = 0.0f;
     for (int s = 0; s < P.splits; ++s) v += load_partial(&P.partials[(int64_t)s * P.n * P.m + o], P.finish);
+    // leave the workspace at zero for the calls that share it
+    for (int s = 0; s < P.splits; ++s) store_partial(&P.partials[(int64_t)s * P.n * P.m + o], 0.0f, P.finish);
     P.y[o] = v;
   }
   if (tid == 0) __hip_atomic_store(&P.counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -755,27 +757,77 @@ __device__ __forceinline__ void store_sc1(float* p, float4_t v) {
   asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
 }
 
-// Eight independent sc1 loads in flight, then one wait.
-__device__ __forceinline__ void load8_sc1(float4_t (&t)[8], const float* const (&a)[8]) {
+// Partials of the in-kernel hand-off travel encoded: each word is the bitwise
+// complement of the value, NaN first made the canonical 0x7FC00000, so a word
+// of zero (the complement of 0xFFFFFFFF, a NaN pattern that never reaches the
+// encoder) means "not written yet".  The owner of a tile group clears the
+// words it consumed, which leaves every slot at zero for the next call.
+__device__ __forceinline__ float4_t enc_partial(float4_t v) {
+  float4_t e;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t b = __builtin_isnan(v[i]) ? 0x7FC00000u : __float_as_uint(v[i]);
+    e[i] = __uint_as_float(~b);
+  }
+  return e;
+}
+
+__device__ __forceinline__ bool partial_ready(float4_t w) {
+  return __float_as_uint(w[0]) != 0u && __float_as_uint(w[1]) != 0u && __float_as_uint(w[2]) != 0u &&
+         __float_as_uint(w[3]) != 0u;
+}
+
+__device__ __forceinline__ float4_t dec_partial(float4_t w) {
+  float4_t v;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = __uint_as_float(~__float_as_uint(w[i]));
+  return v;
+}
+
+// Repeated batch loads a thread of the owner may spend on chunks not yet
+// written before it stops waiting and adds them as they read (NaN): about a
+// second, a bound on the wait that contributors, which store their partials
+// before they wait for anything, never let it reach.
+constexpr int kMaxPolls = 1 << 19;
+
+// Sixteen independent sc1 loads in flight, then one wait: base (scalar) +
+// per-lane 32-bit byte offsets.
+__device__ __forceinline__ void load16_sc1(float4_t (&t)[16], const float* base, const uint32_t (&o)[16]) {
   asm volatile(
-      "global_load_dwordx4 %0, %8, off sc1\n\t"
-      "global_load_dwordx4 %1, %9, off sc1\n\t"
-      "global_load_dwordx4 %2, %10, off sc1\n\t"
-      "global_load_dwordx4 %3, %11, off sc1\n\t"
-      "global_load_dwordx4 %4, %12, off sc1\n\t"
-      "global_load_dwordx4 %5, %13, off sc1\n\t"
-      "global_load_dwordx4 %6, %14, off sc1\n\t"
-      "global_load_dwordx4 %7, %15, off sc1\n\t"
+      "global_load_dwordx4 %0, %16, %32 sc1\n\t"
+      "global_load_dwordx4 %1, %17, %32 sc1\n\t"
+      "global_load_dwordx4 %2, %18, %32 sc1\n\t"
+      "global_load_dwordx4 %3, %19, %32 sc1\n\t"
+      "global_load_dwordx4 %4, %20, %32 sc1\n\t"
+      "global_load_dwordx4 %5, %21, %32 sc1\n\t"
+      "global_load_dwordx4 %6, %22, %32 sc1\n\t"
+      "global_load_dwordx4 %7, %23, %32 sc1\n\t"
+      "global_load_dwordx4 %8, %24, %32 sc1\n\t"
+      "global_load_dwordx4 %9, %25, %32 sc1\n\t"
+      "global_load_dwordx4 %10, %26, %32 sc1\n\t"
+      "global_load_dwordx4 %11, %27, %32 sc1\n\t"
+      "global_load_dwordx4 %12, %28, %32 sc1\n\t"
+      "global_load_dwordx4 %13, %29, %32 sc1\n\t"
+      "global_load_dwordx4 %14, %30, %32 sc1\n\t"
+      "global_load_dwordx4 %15, %31, %32 sc1\n\t"
       "s_waitcnt vmcnt(0)"
-      : "=&v"(t[0]), "=&v"(t[1]), "=&v"(t[2]), "=&v"(t[3]), "=&v"(t[4]), "=&v"(t[5]), "=&v"(t[6]), "=&v"(t[7])
-      : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(a[4]), "v"(a[5]), "v"(a[6]), "v"(a[7])
+      : "=&v"(t[0]), "=&v"(t[1]), "=&v"(t[2]), "=&v"(t[3]), "=&v"(t[4]), "=&v"(t[5]), "=&v"(t[6]), "=&v"(t[7]),
+        "=&v"(t[8]), "=&v"(t[9]), "=&v"(t[10]), "=&v"(t[11]), "=&v"(t[12]), "=&v"(t[13]), "=&v"(t[14]),
+        "=&v"(t[15])
+      : "v"(o[0]), "v"(o[1]), "v"(o[2]), "v"(o[3]), "v"(o[4]), "v"(o[5]), "v"(o[6]), "v"(o[7]), "v"(o[8]),
+        "v"(o[9]), "v"(o[10]), "v"(o[11]), "v"(o[12]), "v"(o[13]), "v"(o[14]), "v"(o[15]), "s"(base)
       : "memory");
+}
+
+__device__ __forceinline__ void store_sc1_at(float* base, uint32_t o, float4_t v) {
+  asm volatile("global_store_dwordx4 %0, %1, %2 sc1" : : "v"(o), "v"(v), "s"(base) : "memory");
 }
 
 // Output of a tile group: tile tl of the group sums `nslots` LDS slots
 // (slot s of tile tl at red + (tl * nslots + s) * per_slot) and goes to Y
-// (part == nullptr) or to the partial slot part + tl * per_slot.  The whole
-// workgroup stores, one 4-column quad per thread and step.
+// (part == nullptr) or to the partial slot part + tl * per_slot, plain (for
+// the fix-up kernel) or encoded and device-coherent (for the owner of the
+// group).  The whole workgroup stores, one 4-column quad per thread and step.
 template <int kC, int kW>
 __device__ __forceinline__ void rec_store(const GemmParams& P, const float* red, int per_slot, int nslots, int tg,
                                           float* part, bool coherent) {
@@ -792,7 +844,7 @@ __device__ __forceinline__ void rec_store(const GemmParams& P, const float* red,
     for (int sl = 1; sl < nslots; ++sl) v += *reinterpret_cast<const float4_t*>(base + sl * per_slot);
     if (part) {
       float* pp = part + tl * per_slot + row * kRecCols + 4 * qd;
-      if (coherent) store_sc1(pp, v);
+      if (coherent) store_sc1(pp, enc_partial(v));
       else *reinterpret_cast<float4_t*>(pp) = v;
     } else {
       float* yp = P.y + (int64_t)row * P.m + m0 + 4 * qd;
@@ -806,58 +858,110 @@ __device__ __forceinline__ void rec_store(const GemmParams& P, const float* red,
   }
 }
 
-// In-kernel hand-off of a shared tile group: this workgroup's partials are
-// written (sc1) and acknowledged, then one agent-scope counter per group
-// counts the contributors; the last one adds every contributor's partials in
-// workgroup order (sc1 loads, eight in flight), writes Y and clears the
-// counter for the next call.
-template <int kC, int kW>
-__device__ __forceinline__ void rec_handoff(const GemmParams& P, int tg) {
-  __shared__ int s_last;
-  asm volatile("s_waitcnt vmcnt(0)" : : : "memory");  // this thread's partial stores are complete
-  __syncthreads();
+// In-kernel hand-off, run by the owner of a shared tile group (the workgroup
+// whose range holds the group's last round; it processes that segment last,
+// after every contribution it makes to other groups).  The contributors
+// p0 .. owner-1 have stored their partials encoded, each before any wait of
+// its own; the owner reads them device-coherently, polls again while any
+// word reads "not written", adds them in workgroup order and its own partial
+// (the LDS slots) last -- the fix-up kernel's order, so both hand-offs give
+// the same bits -- writes Y and clears the chunks it read.
+//
+// A thread takes kQ of its quads at a time and kCB contributors of each: the
+// kQ * kCB = 16 loads go out together, one memory round trip per batch.
+template <int kQ, int kCB, int kC, int kW>
+__device__ __forceinline__ void rec_gather_batched(const GemmParams& P, const float* red, int per_slot, int nslots,
+                                                   int tg, int owner, int p0, int& polls) {
+  static_assert(kQ * kCB == 16, "one batch is 16 loads");
   const int item0 = tg * P.rounds;
-  const int p0 = streamk_owner(P, item0), p1 = streamk_owner(P, item0 + P.rounds - 1);
-  if (threadIdx.x == 0) {
-    const uint32_t prev = __hip_atomic_fetch_add(&P.counters[tg], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = prev == (uint32_t)(p1 - p0);
-  }
-  __syncthreads();
-  if (!s_last) return;
-  const int per_slot = P.n * kRecCols;
   const int total = kC * P.n * 64;
-  for (int idx = threadIdx.x; idx < total; idx += kW * 64) {
-    const int tl = kC == 1 ? 0 : idx / (P.n * 64);
-    const int w = idx - tl * P.n * 64;
-    const int row = w >> 6, qd = w & 63;
-    const int m0 = (tg * kC + tl) * kRecCols;
-    if (m0 + 4 * qd >= P.m) continue;
-    const int64_t off = (int64_t)tl * per_slot + row * kRecCols + 4 * qd;
-    float4_t v = {0.f, 0.f, 0.f, 0.f};
-    for (int p8 = p0; p8 <= p1; p8 += 8) {
-      const float* a[8];
+  const float4_t zero = {0.f, 0.f, 0.f, 0.f};
+  const uint32_t slot_bytes = (uint32_t)(kC * per_slot * sizeof(float));  // partials of one workgroup segment
+  for (int first = threadIdx.x; first < total; first += kQ * kW * 64) {
+    uint32_t off[kQ];  // byte offset of quad j inside a slot
+    bool ok[kQ];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int pp = min(p8 + i, p1);  // past the end: re-read the last one, added as 0 below
-        const int lo_p = pp * P.items_base + min(pp, P.items_rem);
-        const int pslot = 2 * pp + (lo_p < item0 ? 1 : 0);
-        a[i] = P.partials + (int64_t)pslot * kC * per_slot + off;
-      }
-      float4_t t[8];
-      load8_sc1(t, a);
-#pragma unroll
-      for (int i = 0; i < 8; ++i)  // in workgroup order
-        if (p8 + i <= p1) v += t[i];
+    for (int j = 0; j < kQ; ++j) {
+      const int idx = first + j * kW * 64;
+      const int tl = kC == 1 ? 0 : idx / (P.n * 64);
+      const int w = idx - tl * P.n * 64;
+      const int row = w >> 6, qd = w & 63;
+      ok[j] = idx < total && (tg * kC + tl) * kRecCols + 4 * qd < P.m;
+      off[j] = ok[j] ? (uint32_t)(4 * (tl * per_slot + row * kRecCols + 4 * qd)) : 0u;  // outside: a harmless read
     }
-    float* yp = P.y + (int64_t)row * P.m + m0 + 4 * qd;
-    if (P.y_vec) {
-      *reinterpret_cast<float4_t*>(yp) = v;
-    } else {
+    float4_t v[kQ];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) yp[e] = v[e];
+    for (int j = 0; j < kQ; ++j) v[j] = zero;
+    for (int c0 = p0; c0 < owner; c0 += kCB) {
+      uint32_t a[16];
+#pragma unroll
+      for (int i = 0; i < kCB; ++i) {
+        const int pp = min(c0 + i, owner - 1);  // past the last contributor: re-read it, not added
+        const int lo_p = pp * P.items_base + min(pp, P.items_rem);
+        const uint32_t slot = (uint32_t)(2 * pp + (lo_p < item0 ? 1 : 0)) * slot_bytes;
+#pragma unroll
+        for (int j = 0; j < kQ; ++j) a[j * kCB + i] = slot + off[j];
+      }
+      float4_t t[16];
+      load16_sc1(t, P.partials, a);
+      // a chunk still unwritten: load the whole batch again (one round trip
+      // for all of them) after a short sleep
+      for (;;) {
+        bool ready = true;
+#pragma unroll
+        for (int j = 0; j < kQ; ++j)
+#pragma unroll
+          for (int i = 0; i < kCB; ++i)
+            if (ok[j] && c0 + i < owner) ready = ready && partial_ready(t[j * kCB + i]);
+        if (ready || polls <= 0) break;
+        --polls;
+        __builtin_amdgcn_s_sleep(1);
+        load16_sc1(t, P.partials, a);
+      }
+#pragma unroll
+      for (int j = 0; j < kQ; ++j)
+#pragma unroll
+        for (int i = 0; i < kCB; ++i)  // in workgroup order
+          if (ok[j] && c0 + i < owner) v[j] += dec_partial(t[j * kCB + i]);
+#pragma unroll
+      for (int j = 0; j < kQ; ++j)
+#pragma unroll
+        for (int i = 0; i < kCB; ++i)
+          if (ok[j] && c0 + i < owner) store_sc1_at(P.partials, a[j * kCB + i], zero);
+    }
+#pragma unroll
+    for (int j = 0; j < kQ; ++j) {
+      if (!ok[j]) continue;
+      const int idx = first + j * kW * 64;
+      const int tl = kC == 1 ? 0 : idx / (P.n * 64);
+      const int w = idx - tl * P.n * 64;
+      const int row = w >> 6, qd = w & 63;
+      const float* base = red + tl * nslots * per_slot + red_pos(row, qd >> 2, qd & 3);
+      float4_t own = *reinterpret_cast<const float4_t*>(base);
+      for (int sl = 1; sl < nslots; ++sl) own += *reinterpret_cast<const float4_t*>(base + sl * per_slot);
+      v[j] += own;
+      float* yp = P.y + (int64_t)row * P.m + (tg * kC + tl) * kRecCols + 4 * qd;
+      if (P.y_vec) {
+        *reinterpret_cast<float4_t*>(yp) = v[j];
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) yp[e] = v[j][e];
+      }
     }
   }
-  if (threadIdx.x == 0) __hip_atomic_store(&P.counters[tg], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Batch shape by contributor count: as many of a thread's quads per batch as
+// 16 loads allow with every contributor (up to 8) in it.
+template <int kC, int kW>
+__device__ __forceinline__ void rec_gather(const GemmParams& P, const float* red, int per_slot, int nslots, int tg,
+                                           int owner) {
+  const int p0 = streamk_owner(P, tg * P.rounds);
+  int polls = kMaxPolls;  // this thread's budget of repeated loads
+  const int contributors = owner - p0;
+  if (contributors <= 2) rec_gather_batched<8, 2, kC, kW>(P, red, per_slot, nslots, tg, owner, p0, polls);
+  else if (contributors <= 4) rec_gather_batched<4, 4, kC, kW>(P, red, per_slot, nslots, tg, owner, p0, polls);
+  else rec_gather_batched<2, 8, kC, kW>(P, red, per_slot, nslots, tg, owner, p0, polls);
 }
 
 template <int NR, int kDepth, int kC, int kW>
@@ -869,7 +973,7 @@ __global__ void __launch_bounds__(kW * 64) int4_gemm_records_kernel(GemmParams P
   // first use (each late load is another serial trip to memory)
   asm volatile("" : : "s"(P.x), "s"(P.sb), "s"(P.y), "s"(P.partials), "s"(P.n), "s"(P.k), "s"(P.m),
                "s"(P.rounds), "s"(P.shift), "s"(P.y_vec), "s"(P.items_base), "s"(P.items_rem), "s"(P.tiles),
-               "s"(P.counters), "s"(P.finish), "s"(P.splits));
+               "s"(P.finish), "s"(P.splits));
   const int lane = threadIdx.x & 63;
   // wave index as a scalar: the round loop below is then uniform control flow
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -900,10 +1004,16 @@ __global__ void __launch_bounds__(kW * 64) int4_gemm_records_kernel(GemmParams P
     const int chunk = (lane & 3) ^ ((lane >> 2) & 3) ^ ((lane >> 4) & 3);
     xoff[nt] = (uint32_t)(2 * (row * P.k + 8 * chunk));
   }
-  // workgroup ids are dealt round-robin to the 8 XCDs: give each XCD one
-  // contiguous run of ranges, so that the tiles it shares meet in its L2
-  // (the workgroup count is P.splits: the grid size would be one more serial
-  // load from the dispatch's hidden arguments)
+  // Workgroup ids are dealt round-robin to the 8 XCDs: give each XCD one
+  // contiguous run of ranges, so that neighbouring tiles, which share the
+  // 128-byte lines at their edges, meet in its L2.  Within a run the range
+  // order is the dispatch order, so the owner of a tile group (its highest
+  // range, which waits in the in-kernel hand-off) starts after the
+  // contributors it waits for; only a group that straddles two runs (at most
+  // 7) can have an owner dispatched before a contributor, and those few
+  // waiting owners cannot hold back the dispatch of the rest.  (The workgroup
+  // count is P.splits: the grid size would be one more serial load from the
+  // dispatch's hidden arguments.)
   const int nwg = P.splits, b = blockIdx.x, per = nwg / kXcds;
   const int p = b < per * kXcds ? (b % kXcds) * per + b / kXcds : b;
   int lo, hi;
@@ -919,10 +1029,13 @@ __global__ void __launch_bounds__(kW * 64) int4_gemm_records_kernel(GemmParams P
   constexpr int kHalf = kShare >= 2 ? kShare / 2 : 1;
   constexpr int kSlots = kHalf;  // reduction slots per tile
 
-  for (int seg_lo = lo; seg_lo < hi;) {
-    const int tg = seg_lo / P.rounds;
+  // Segments (the range's pieces in one tile group) run from the last to the
+  // first: the segment that ends a tile group (its owner's) then runs last in
+  // its workgroup, and the segments that contribute to it run first in theirs.
+  for (int seg_hi = hi; seg_hi > lo;) {
+    const int tg = (seg_hi - 1) / P.rounds;
+    const int seg_lo = max(lo, tg * P.rounds);
     const int r0 = seg_lo - tg * P.rounds;
-    const int seg_hi = min(hi, (tg + 1) * P.rounds);
     const int r1 = seg_hi - tg * P.rounds;
     const int tile = tg * kC + tl;
     const bool has_tile = tile < P.tiles;  // the last group may be short
@@ -1000,11 +1113,14 @@ __global__ void __launch_bounds__(kW * 64) int4_gemm_records_kernel(GemmParams P
     const bool whole = r0 == 0 && r1 == P.rounds;
     const int pslot = 2 * p + (seg_lo == lo ? 0 : 1);
     const bool in_kernel = P.finish != kFinishSecondKernel;
-    rec_store<kC, kW>(P, red, per_slot, kSlots, tg, whole ? nullptr : P.partials + (int64_t)pslot * kC * per_slot,
-                      in_kernel);
-    if (!whole && in_kernel) rec_handoff<kC, kW>(P, tg);
+    if (!whole && in_kernel && r1 == P.rounds) {
+      rec_gather<kC, kW>(P, red, per_slot, kSlots, tg, p);  // this workgroup owns the group
+    } else {
+      rec_store<kC, kW>(P, red, per_slot, kSlots, tg,
+                        whole ? nullptr : P.partials + (int64_t)pslot * kC * per_slot, in_kernel);
+    }
     __syncthreads();  // LDS is the next segment's ring
-    seg_lo = seg_hi;
+    seg_hi = seg_lo;
   }
 }
 
@@ -1029,16 +1145,21 @@ __global__ void __launch_bounds__(256) streamk_fixup_kernel(GemmParams P, int gr
     const int64_t off = (int64_t)tl * per_slot + row * kRecCols + 4 * qd;
     for (int p8 = p0; p8 <= p1; p8 += 8) {
       float4_t t[8];
+      float4_t* a[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const int pp = min(p8 + i, p1);  // past the end: re-read the last one, added as 0 below
         const int lo_p = pp * P.items_base + min(pp, P.items_rem);
         const int pslot = 2 * pp + (lo_p < item0 ? 1 : 0);
-        t[i] = *reinterpret_cast<const float4_t*>(P.partials + (int64_t)pslot * group_tiles * per_slot + off);
+        a[i] = reinterpret_cast<float4_t*>(P.partials + (int64_t)pslot * group_tiles * per_slot + off);
+        t[i] = *a[i];
       }
 #pragma unroll
       for (int i = 0; i < 8; ++i)  // in workgroup order
         if (p8 + i <= p1) v += t[i];
+#pragma unroll
+      for (int i = 0; i < 8; ++i)  // leave the slots at zero (the in-kernel hand-off reads zero as empty)
+        if (p8 + i <= p1) *a[i] = float4_t{0.f, 0.f, 0.f, 0.f};
     }
     float* yp = P.y + (int64_t)row * P.m + m0 + 4 * qd;
     if (P.y_vec) {
@@ -1051,8 +1172,8 @@ __global__ void __launch_bounds__(256) streamk_fixup_kernel(GemmParams P, int gr
 }
 
 // Second kernel of kFinishSecondKernel: y = sum over splits of the partials.
-__global__ void __launch_bounds__(256) splitk_sum_kernel(const float* __restrict__ partials, int splits,
-                                                         int64_t nm, float* __restrict__ y) {
+__global__ void __launch_bounds__(256) splitk_sum_kernel(float* __restrict__ partials, int splits, int64_t nm,
+                                                         float* __restrict__ y) {
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nm; i += stride) {
     // 8 independent loads in flight before any add, summed in split order
@@ -1064,6 +1185,9 @@ __global__ void __launch_bounds__(256) splitk_sum_kernel(const float* __restrict
 #pragma unroll
       for (int k = 0; k < 8; ++k)
         if (s8 + k < splits) v += t[k];
+#pragma unroll
+      for (int k = 0; k < 8; ++k)  // leave the workspace at zero for the calls that share it
+        if (s8 + k < splits) partials[(int64_t)(s8 + k) * nm + i] = 0.0f;
     }
     y[i] = v;
   }
@@ -1160,14 +1284,6 @@ static hipError_t launch_records(const GemmParams& P, int wgs, int depth, int gr
 bool gemm_records_eligible(int k, int m) { return (m % 128) == 0 && (k % kRoundRows) == 0; }
 
 // Dynamic LDS of one record-stream workgroup (after the depth clamp).
-size_t gemm_records_lds(int n, int depth, int group_tiles, int waves) {
-  const size_t stage = n <= 16 ? RecGeom<1>::kStageBytes : RecGeom<2>::kStageBytes;
-  const int max_depth = (int)(kMaxDynamicLds / (waves * stage));
-  if (depth > max_depth) depth = max_depth;
-  const size_t ring = (size_t)waves * depth * stage;
-  const size_t red = (size_t)group_tiles * rec_slots_per_tile(waves, group_tiles) * n * kRecCols * sizeof(float);
-  return ring > red ? ring : red;
-}
 int gemm_records_tiles(int m) { return (m + kRecCols - 1) / kRecCols; }
 int gemm_records_groups(int m, int group_tiles) { return (gemm_records_tiles(m) + group_tiles - 1) / group_tiles; }
 

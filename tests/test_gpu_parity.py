@@ -183,8 +183,9 @@ def test_gemm_record_stream_kernel(K, M):
 
 
 def test_gemm_workspace_shared_between_kernels():
-    """Calls of both kernels alternate on one stream, hence one workspace:
-    the record-stream partials must leave the split-K counter block zero."""
+    """Calls of both kernels and of every hand-off alternate on one stream,
+    hence one workspace: each must leave it all at zero (the record-stream
+    kernel's in-kernel hand-off reads zero as "partial not written")."""
     from moat_amd.dequant import batched_int4_matmul
     L = _lib()
     K, M = 2048, 5504
@@ -198,7 +199,8 @@ def test_gemm_workspace_shared_between_kernels():
         xd = torch.from_numpy(x).cuda()
         for rep in range(3):
             for front, splits, finish in ((L.FRONT_RECORDS, 8, 0), (L.FRONT_LDS, 3, 1), (L.FRONT_RECORDS, 3, 0),
-                                          (L.FRONT_DIRECT, 5, 2)):
+                                          (L.FRONT_DIRECT, 5, 2), (L.FRONT_RECORDS, 176, 0), (L.FRONT_LDS, 4, 3),
+                                          (L.FRONT_RECORDS, 5, 3), (L.FRONT_RECORDS, 44, 0)):
                 say(f"case: shared workspace N={N} rep={rep} front={front} splits={splits} finish={finish}")
                 y = batched_int4_matmul(xd, blob_d, K, M, algo=L.GEMM_MFMA, splits=splits, finish=finish, front=front)
                 assert rel_err(y.cpu().numpy(), yref) <= TOL, (N, rep, front, splits, finish)
@@ -279,15 +281,16 @@ def test_gemm_split_k_handoff_is_deterministic():
     K, M, _, blob = workload("ffn 2048x5504")
     blob_d = torch.from_numpy(blob.reshape(-1)).cuda()
     L = _lib()
-    for front in (L.FRONT_RECORDS, L.FRONT_LDS):
+    for front, splits in ((L.FRONT_RECORDS, 16), (L.FRONT_RECORDS, 176), (L.FRONT_RECORDS, 500),
+                          (L.FRONT_LDS, 16)):
         for N in (1, 4, 32):
             x = torch.from_numpy(_x(N, K, 3)).cuda()
-            ref = batched_int4_matmul(x, blob_d, K, M, algo=2, splits=16, finish=3, front=front)
-            for finish in (1, 2, 3):
-                say(f"case: split-K hand-off front={front} N={N} finish={finish}")
+            ref = batched_int4_matmul(x, blob_d, K, M, algo=2, splits=splits, finish=3, front=front)
+            for finish in (0, 1, 2, 3):
+                say(f"case: split-K hand-off front={front} splits={splits} N={N} finish={finish}")
                 for _ in range(20):
-                    y = batched_int4_matmul(x, blob_d, K, M, algo=2, splits=16, finish=finish, front=front)
-                    assert torch.equal(y, ref), (front, N, finish)
+                    y = batched_int4_matmul(x, blob_d, K, M, algo=2, splits=splits, finish=finish, front=front)
+                    assert torch.equal(y, ref), (front, splits, N, finish)
 
 
 def test_gemm_n_above_32_is_sliced():
