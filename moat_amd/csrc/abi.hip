@@ -136,6 +136,15 @@ GemmPlan plan_gemm(int32_t n, int32_t k, int32_t m, const moat_int4_gemm_options
       if (by_traffic < 2) by_traffic = 2;
       if (splits > by_traffic) splits = by_traffic;
       if (splits < 1) splits = 1;
+      // prefer a count that divides the rounds: every workgroup then holds
+      // one segment of one tile group (a range that crosses a group boundary
+      // costs a second segment, measured ~3 us per call)
+      for (int64_t s = splits; s * 2 >= splits; --s) {
+        if (rounds % s == 0) {
+          splits = s;
+          break;
+        }
+      }
     }
     int64_t wgs = (int64_t)groups * splits;
     const int64_t items = (int64_t)groups * rounds;

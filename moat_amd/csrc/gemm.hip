@@ -1026,8 +1026,7 @@ __global__ void __launch_bounds__(kW * 64) int4_gemm_records_kernel(GemmParams P
   const uint32_t ring_lds = (uint32_t)(uintptr_t)(lds_ptr_t)ring;  // LDS byte address (wave-uniform)
   float* red = reinterpret_cast<float*>(smem);
   const int per_slot = P.n * kRecCols;
-  constexpr int kHalf = kShare >= 2 ? kShare / 2 : 1;
-  constexpr int kSlots = kHalf;  // reduction slots per tile
+  constexpr int kSlots = kShare;  // reduction slots per tile: one per wave
 
   // Segments (the range's pieces in one tile group) run from the last to the
   // first: the segment that ends a tile group (its owner's) then runs last in
@@ -1078,38 +1077,28 @@ __global__ void __launch_bounds__(kW * 64) int4_gemm_records_kernel(GemmParams P
     }
     __syncthreads();  // the ring is reused for the reduction
 
-    // Waves of one tile add up through LDS: the upper half of its waves
-    // (kpart >= kShare / 2) store into the tile's kShare / 2 slots, the lower
-    // half add theirs, and the store below sums the slots; a single wave
-    // per tile just stores.  Lane (q, j) holds D[16*nt + 4q + v][16j + c];
-    // 4 columns per access.
-    float* tred = red + tl * kSlots * per_slot;
-    constexpr int kPhases = kShare > 1 ? 2 : 1;
+    // Waves of one tile add up through LDS: each stores its accumulators in
+    // its own slot of the tile, and the store below sums the slots in wave
+    // order.  Lane (q, j) holds D[16*nt + 4q + v][16j + c]; 4 columns per
+    // access.
+    {
+      float* slot = red + (tl * kSlots + kpart) * per_slot;
 #pragma unroll
-    for (int phase = 0; phase < kPhases; ++phase) {
-      const bool active = kShare == 1 ? true : (phase == 0 ? kpart >= kHalf : kpart < kHalf);
-      const bool add = kShare > 1 && phase == 1;
-      if (active) {
-        float* slot = tred + (kpart % kHalf) * per_slot;
+      for (int nt = 0; nt < NR; ++nt)
 #pragma unroll
-        for (int nt = 0; nt < NR; ++nt)
+        for (int v = 0; v < 4; ++v) {
+          const int row = nt * 16 + 4 * q + v;
+          if (row < P.n) {
 #pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            const int row = nt * 16 + 4 * q + v;
-            if (row < P.n) {
-#pragma unroll
-              for (int u = 0; u < 4; ++u) {
-                float4_t* pp = reinterpret_cast<float4_t*>(slot + red_pos(row, j, u));
-                float4_t val = {acc.c[nt][4 * u][v], acc.c[nt][4 * u + 1][v], acc.c[nt][4 * u + 2][v],
-                                acc.c[nt][4 * u + 3][v]};
-                if (add) val += *pp;
-                *pp = val;
-              }
+            for (int u = 0; u < 4; ++u) {
+              const float4_t val = {acc.c[nt][4 * u][v], acc.c[nt][4 * u + 1][v], acc.c[nt][4 * u + 2][v],
+                                    acc.c[nt][4 * u + 3][v]};
+              *reinterpret_cast<float4_t*>(slot + red_pos(row, j, u)) = val;
             }
           }
-      }
-      __syncthreads();
+        }
     }
+    __syncthreads();
     const bool whole = r0 == 0 && r1 == P.rounds;
     const int pslot = 2 * p + (seg_lo == lo ? 0 : 1);
     const bool in_kernel = P.finish != kFinishSecondKernel;
@@ -1237,10 +1226,8 @@ static hipError_t launch_front(const GemmParams& P, int algo, int batch, hipStre
   return launch_gemm_variant<1, kFront>(P, algo, stream);
 }
 
-// Reduction slots of one tile: half the waves that share it (one at least).
-constexpr int rec_slots_per_tile(int waves, int group_tiles) {
-  return waves / group_tiles >= 2 ? waves / group_tiles / 2 : 1;
-}
+// Reduction slots of one tile: one per wave that shares it.
+constexpr int rec_slots_per_tile(int waves, int group_tiles) { return waves / group_tiles; }
 
 template <int NR, int kDepth, int kC, int kW>
 static hipError_t launch_records_one(const GemmParams& P, int wgs, hipStream_t stream) {
