@@ -39,6 +39,12 @@ WORKLOAD_NAMES = {
     "k8192_m28672": "int4 superblock projection K=8192 M=28672 (70B-class FFN, 0.1% 8-sigma outliers)",
 }
 ROTATE_BYTES = 300 * 1024 * 1024
+# One decoder layer's projections at hidden 2048 (Q, K, V, O 2048x2048; gate
+# and up 2048x5632; down 5632 -> 2048), run back to back at N = 16 traces.
+LAYER = [("q", 2048, 2048), ("k", 2048, 2048), ("v", 2048, 2048), ("o", 2048, 2048),
+         ("gate", 2048, 5632), ("up", 2048, 5632), ("down", 5632, 2048)]
+LAYER_N = 16
+LAYER_SEED = 1004
 
 
 def log(*a):
@@ -129,7 +135,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="k2048_m5504", choices=sorted(CONFIGS))
+    ap.add_argument("--config", default="k2048_m5504", choices=sorted(CONFIGS) + ["layer_h2048"],
+                    help="projection shape, or layer_h2048: one decoder layer's 7 projections at N=16")
     ap.add_argument("--ns", default=None, help="comma-separated N values (default: the config's)")
     ap.add_argument("--algo", type=int, default=0, help="0 auto, 1 dot2, 2 mfma")
     ap.add_argument("--splits", type=int, default=0)
@@ -140,6 +147,8 @@ def main() -> int:
     ap.add_argument("--finish", type=int, default=0, help="split-K hand-off (0 auto, 1 atomics, 2 fences, 3 kernel)")
     ap.add_argument("--front", type=int, default=0,
                     help="load front end (0 auto, 1 LDS-staged, 2 direct, 3 LDS DMA, 4 record stream)")
+    ap.add_argument("--fused", action="store_true",
+                    help="layer_h2048: Q, K, V in one launch and gate/up fused with SwiGLU (h feeds down)")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"), default=None,
                     help="no GPU run: turn two rocprofv3 --pmc counter CSVs (FETCH_SIZE, WRITE_SIZE) of "
                          "`bench.py --ns N` into profiles/traffic_<config>.json")
@@ -160,6 +169,9 @@ def main() -> int:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})",
               file=sys.stderr)
         return 2
+
+    if args.config == "layer_h2048":
+        return run_layer(args)
 
     import torch
     from moat_amd import _lib
@@ -303,6 +315,155 @@ def main() -> int:
                    "activations": "fp16", "output": "fp32"},
         "per_n": {str(k): v for k, v in per_n.items()},
         "roofline": roof,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+def run_layer(args) -> int:
+    """One decoder layer's projections (Q, K, V, O, gate, up, down) at N = 16,
+    back to back on one stream, each on its own weights; the layer's weights
+    rotate over enough copies (>= 300 MB) that no projection is served from
+    the Infinity Cache.  A step is one layer."""
+    import torch
+    from moat_amd import _lib
+    from moat_amd.dequant import _gemm_into, _multi_into, _swiglu_into, quantize_to_superblocks
+
+    _lib.load()
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    N = int(args.ns.split(",")[0]) if args.ns else LAYER_N
+    rng = np.random.default_rng(LAYER_SEED)
+    layer_bytes = sum(144 * K * M // 256 for _, K, M in LAYER)
+    copies = max(2, -(-ROTATE_BYTES // layer_bytes))
+    log(f"[bench] building layer_h2048: 7 projections, {layer_bytes / 1e6:.2f} MB of records, {copies} copies")
+    blobs = []  # blobs[c][p]
+    first = []
+    for name, K, M in LAYER:
+        w = rng.standard_normal((K, M), dtype=np.float32) * np.float32(0.02)
+        first.append(quantize_to_superblocks(torch.from_numpy(w).to(dev)))
+    blobs.append(first)
+    for c in range(1, copies):
+        blobs.append([b.clone() for b in first])
+    xs = [torch.from_numpy(np.random.default_rng(2400 + i).standard_normal((N, K), dtype=np.float32)
+                           .astype(np.float16)).to(dev) for i, (_, K, M) in enumerate(LAYER)]
+    ys = [torch.empty((N, M), dtype=torch.float32, device=dev) for _, K, M in LAYER]
+
+    h = torch.empty((N, 5632), dtype=torch.float16, device=dev)
+
+    def layer(c):
+        b = blobs[c % copies]
+        if args.fused:
+            # Q, K, V: one launch on the shared input; O; gate/up + SwiGLU -> h; down(h)
+            _multi_into(xs[0], b[0:3], ys[0:3], 2048, 2048)
+            _gemm_into(xs[3], b[3], ys[3], 2048, 2048)
+            _swiglu_into(xs[4], b[4], b[5], h, 2048, 5632)
+            _gemm_into(h, b[6], ys[6], 5632, 2048)
+            return
+        for p, (_, K, M) in enumerate(LAYER):
+            _gemm_into(xs[p], b[p], ys[p], K, M, args.algo, args.splits, args.batch, args.finish, args.front)
+
+    cap = torch.cuda.Stream()
+    cap.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(cap):
+        for c in range(2):
+            layer(c)
+    torch.cuda.synchronize()
+    # one graph holds one layer on every weight copy (`copies` layers)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=cap):
+        for c in range(copies):
+            layer(c)
+    torch.cuda.synchronize()
+
+    def timed(replays):
+        with torch.cuda.stream(cap):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(cap)
+            for r in range(replays):
+                graph.replay()
+            e1.record(cap)
+        e1.synchronize()
+        return e0.elapsed_time(e1) * 1e3  # us
+
+    warm_us = timed(1)
+    timed(max(1, int(20000 / max(warm_us, 1.0))))  # about 20 ms at full clocks
+    replays = max(1, -(-args.steps // copies))
+    us = timed(replays) / (replays * copies)
+    value = N / (us / 1e6)
+    bytes_layer = sum(algo_bytes(N, K, M) for _, K, M in LAYER)
+    if args.fused:  # X read once by Q/K/V and by gate/up; h (fp16) written once instead of gate and up
+        bytes_layer -= 2 * (2 * N * 2048) + 2 * 4 * N * 5632 - 2 * N * 5632
+    log(f"[bench] layer{' (fused)' if args.fused else ''}: {us:.2f} us/layer, {value:.0f} tok/s, "
+        f"{bytes_layer / us / 1e3:.0f} GB/s")
+
+    # per projection: one graph of that projection on every weight copy
+    per_proj = {}
+    for p, (name, K, M) in enumerate(LAYER):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=cap):
+            for c in range(copies):
+                _gemm_into(xs[p], blobs[c][p], ys[p], K, M, args.algo, args.splits, args.batch, args.finish,
+                           args.front)
+        torch.cuda.synchronize()
+        reps = max(2, args.calls // copies)
+        with torch.cuda.stream(cap):
+            g.replay()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(cap)
+            for r in range(reps):
+                g.replay()
+            e1.record(cap)
+        e1.synchronize()
+        pus = e0.elapsed_time(e1) * 1e3 / (reps * copies)
+        b = algo_bytes(N, K, M)
+        per_proj[name] = {"K": K, "M": M, "us_per_call": round(pus, 3), "gbs": round(b / pus / 1e3, 1),
+                          "roofline_frac": round(b / pus / 1e3 / HBM_PEAK_GBS, 4)}
+        log(f"[bench] {name:4s} {K}x{M}: {pus:7.2f} us/call  {b / pus / 1e3:6.0f} GB/s")
+        del g
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+        from oracle import superblock_oracle as O
+        hosts = [(first[p].cpu().numpy(), xs[p].cpu().numpy(), K, M) for p, (_, K, M) in enumerate(LAYER)]
+        times = []
+        t_start = time.perf_counter()
+        while len(times) < 3 or (time.perf_counter() - t_start < args.cpu_budget and len(times) < 10):
+            t0 = time.perf_counter()
+            for blob_h, x_h, K, M in hosts:
+                O.gemm_ref(x_h, blob_h, K, M)
+            times.append(time.perf_counter() - t0)
+        med = float(np.median(times))
+        cpu = {"value": N / med, "unit": "tok/s", "cores": os.cpu_count(), "kind": "port",
+               "sample": (f"numpy oracle: the 7 projections of one layer (decode records, float32 matmul) at "
+                          f"N={N}, median of {len(times)} layers; host os.cpu_count()={os.cpu_count()}")}
+        log(f"[bench] CPU baseline: {cpu['value']:.1f} tok/s")
+
+    out = {
+        "metric": "INT4 dequant-GEMM µs/call, HBM GB/s (% roofline), tok/s at N=1..32",
+        "value": round(value, 1),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(us / 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic",
+        "config": {"workload": "decoder layer projections at hidden 2048 (Q,K,V,O 2048x2048, gate/up 2048x5632, "
+                               f"down 5632x2048), N={N}, back to back"
+                               + (", Q/K/V in one launch, gate/up fused with SwiGLU" if args.fused else ""),
+                   "n": N, "fused": bool(args.fused),
+                   "weight_copies_rotated": copies, "timing": "HIP graph replay, HIP events on the launch stream",
+                   "weights": "int4 superblocks (144 B per 256 weights)", "activations": "fp16", "output": "fp32"},
+        "per_projection": per_proj,
+        "roofline": {"bound": "hbm", "achieved": round(bytes_layer / us / 1e3, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(bytes_layer / us / 1e3 / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": f"7 projections: {bytes_layer} algorithmic B per layer / {us:.2f} us per layer"},
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

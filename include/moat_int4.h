@@ -142,6 +142,43 @@ int32_t moat_int4_gemm_ex(const uint16_t* x_f16, const uint8_t* superblocks, flo
 int32_t moat_int4_workspace_clear(void* workspace, int64_t bytes, hipStream_t stream);
 
 /*
+ * Several projections of one shape that share their activations, in one
+ * launch: y_f32[i] = f32(x) @ f32(deq(W_i)) for i < count (count 1..4), the
+ * record-stream kernel over the concatenated column tiles.  Replaces
+ * back-to-back dispatchGEMM calls on one input, e.g. the Q, K and V
+ * projections of antigravity-engine/src/transformer_engine.mm:589-596 (one
+ * call for Q, K, V when they have one width; K and V together when grouped
+ * queries make them narrower); each product has moat_int4_gemm's semantics
+ * and tolerance.
+ * `superblocks` and `y_f32` are host arrays of `count` device pointers.
+ * Preconditions: those of moat_int4_gemm, and m % 128 == 0, k % 32 == 0, x
+ * 16-byte aligned (the record-stream kernel's shapes); otherwise
+ * MOAT_ERR_INVALID (call moat_int4_gemm per matrix).  Workspace as for
+ * moat_int4_gemm, sized by moat_int4_gemm_multi_workspace_size.
+ */
+int64_t moat_int4_gemm_multi_workspace_size(int32_t count, int32_t n, int32_t k, int32_t m);
+int32_t moat_int4_gemm_multi(const uint16_t* x_f16, const uint8_t* const* superblocks, float* const* y_f32,
+                             int32_t count, int32_t n, int32_t k, int32_t m,
+                             void* workspace, int64_t workspace_bytes, hipStream_t stream);
+
+/*
+ * Gate and up projections of a SwiGLU MLP fused with the activation:
+ * h = fp16(silu(g) * u), g = f32(x) @ f32(deq(W_gate)), u = f32(x) @
+ * f32(deq(W_up)), silu(g) = g / (1 + exp(-g)) in fp32.  Replaces the two
+ * dispatchGEMM calls and silu_elementwise_mul_kernel of
+ * antigravity-engine/src/transformer_engine.mm:694-713
+ * (antigravity-engine/src/shaders/transformer_ops.metal:216-232; the
+ * reference rounds g and u to fp16 first, this keeps them in fp32).  h is
+ * [n][m] fp16, 8-byte aligned: the down projection's input.  Preconditions
+ * and workspace as for moat_int4_gemm_multi.
+ */
+int64_t moat_int4_gemm_swiglu_workspace_size(int32_t n, int32_t k, int32_t m);
+int32_t moat_int4_gemm_swiglu(const uint16_t* x_f16, const uint8_t* gate_superblocks,
+                              const uint8_t* up_superblocks, uint16_t* h_f16,
+                              int32_t n, int32_t k, int32_t m,
+                              void* workspace, int64_t workspace_bytes, hipStream_t stream);
+
+/*
  * Group quantizer: for each group of group_size values (w_dtype F32, F16 or F64;
  * F64 is rounded to float32 first, as astype(np.float32) does),
  * alpha = max|w|, s = (alpha == 0 ? 1 : alpha / 7) in float32; q =

@@ -48,6 +48,10 @@ SIGNATURES = {
     "moat_int4_gemm_ex_workspace_size": (_I64, [_I32, _I32, _I32, ctypes.POINTER(GemmOptions)]),
     "moat_int4_gemm_ex": (_I32, [_P, _P, _P, _I32, _I32, _I32, ctypes.POINTER(GemmOptions), _P, _I64, _P]),
     "moat_int4_workspace_clear": (_I32, [_P, _I64, _P]),
+    "moat_int4_gemm_multi_workspace_size": (_I64, [_I32, _I32, _I32, _I32]),
+    "moat_int4_gemm_multi": (_I32, [_P, _P, _P, _I32, _I32, _I32, _I32, _P, _I64, _P]),
+    "moat_int4_gemm_swiglu_workspace_size": (_I64, [_I32, _I32, _I32]),
+    "moat_int4_gemm_swiglu": (_I32, [_P, _P, _P, _P, _I32, _I32, _I32, _P, _I64, _P]),
     "moat_int4_quantize": (_I32, [_P, _I32, _I64, _I32, _I32, _P, _P, _P]),
     "moat_int4_pack_superblocks": (_I32, [_P, _P, _I64, _P, _P]),
     "moat_int4_quantize_pack": (_I32, [_P, _I32, _I64, _I32, _P, _P]),

@@ -28,6 +28,11 @@ bool gemm_records_eligible(int k, int m);
 int gemm_records_tiles(int m);
 int gemm_records_groups(int m, int group_tiles);
 bool gemm_records_shares_tiles(int k, int m, int group_tiles, int wgs);
+bool gemm_groups_shared(int64_t groups, int64_t rounds, int wgs);
+int gemm_fused_groups(int mode, int mats, int m);
+hipError_t launch_gemm_fused(int mode, const uint16_t* x, const uint8_t* const* sbs, float* const* ys, uint16_t* h,
+                             int mats, int n, int k, int m, int wgs, int depth, int finish, float* partials,
+                             hipStream_t stream);
 hipError_t launch_gemm(int algo, const uint16_t* x, const uint8_t* sb, float* y, int n, int k, int m, int splits,
                        int batch, int finish, int front, int group, int waves, float* partials,
                        uint32_t* counters, hipStream_t stream);
@@ -85,6 +90,80 @@ bool options_ok(const moat_int4_gemm_options* o, int32_t n) {
 // idle at these sizes) against partial-sum traffic, which is
 // splits * N * M * 8 bytes against 0.5625 * K * M bytes of weights; it is kept
 // below a quarter of the weight stream.
+// Record-stream launch plan for `groups` tile groups of `group` tiles each
+// (`tiles` tiles in all).  Workgroups: a multiple of the group count (so that
+// the workgroups of neighbouring groups read the same rows at the same time
+// and share 128-byte lines in L2), about 8 rounds per workgroup, at most one
+// per CU, and a K split whose fp32 partials stay well below the weight stream.
+void plan_records(GemmPlan& p, int32_t n, int32_t k, int64_t groups, int64_t tiles, int group, int waves,
+                  const moat_int4_gemm_options& opt) {
+  const int rounds = moat::gemm_rounds(k);
+  // ring depth (LDS: waves x depth x 7 or 8 KB; the launch clamps it to the LDS)
+  const int depth = opt.batch ? opt.batch : (waves == 8 ? 2 : (n <= 16 ? 3 : 2));
+  int64_t splits;
+  if (opt.splits > 0) {
+    splits = opt.splits;
+  } else {
+    // about 8 rounds per workgroup: 2 per wave with 4 waves, 1 with 8
+    splits = (tiles * rounds / 8 + groups / 2) / groups;
+    if (splits > 8) splits = 8;  // beyond 8 the hand-off costs more than the shorter loop saves
+    // no more workgroups than the 256 CUs hold at once (a second wave of
+    // workgroups would double the time): one per CU, as the kernel's
+    // registers (over 128 per lane) leave room for one wave per SIMD with 4
+    // waves per workgroup, two with 8
+    const int64_t resident = 256;
+    const int64_t cap_wgs = resident / groups > 0 ? resident / groups : 1;
+    if (splits > cap_wgs) splits = cap_wgs;
+    // above 16 rows the partial sums (N x 256 floats per workgroup) weigh:
+    // stop at about one workgroup per CU
+    if (n > 16) {
+      const int64_t one_per_cu = 256 / groups > 2 ? 256 / groups : 2;
+      if (splits > one_per_cu) splits = one_per_cu;
+    }
+    int64_t by_traffic = k / (16 * n);
+    if (by_traffic < 2) by_traffic = 2;
+    if (splits > by_traffic) splits = by_traffic;
+    if (splits < 1) splits = 1;
+    // prefer a count that divides the rounds: every workgroup then holds
+    // one segment of one tile group (a range that crosses a group boundary
+    // costs a second segment, measured ~3 us per call)
+    for (int64_t s = splits; s * 2 >= splits; --s) {
+      if (rounds % s == 0) {
+        splits = s;
+        break;
+      }
+    }
+  }
+  int64_t wgs = groups * splits;
+  const int64_t items = groups * rounds;
+  if (wgs > items) wgs = items;
+  // the kernel addresses the partials with 32-bit byte offsets
+  const int64_t max_wgs = (int64_t)0xFFFFFFFF / ((int64_t)2 * group * n * 256 * (int64_t)sizeof(float));
+  if (wgs > max_wgs) wgs = max_wgs;
+  p.splits = (int)wgs;
+  p.group = group;
+  p.waves = waves;
+  p.batch = depth;
+  // shared tile groups: summed in the kernel by the workgroup that owns the
+  // group (MOAT_FINISH_DEVICE_ATOMICS or MOAT_FINISH_FENCES) or by a fix-up
+  // kernel (MOAT_FINISH_SECOND_KERNEL).  Automatic: in the kernel while the
+  // owner reads at most 64 KB of partials (n x 1 KB per tile and
+  // contributor), which saves the second launch; beyond that the owner's
+  // one CU is slower than the fix-up kernel spread over many.
+  if (opt.finish == MOAT_FINISH_AUTO) {
+    const int64_t per_group = (wgs + groups - 1) / groups;  // workgroups sharing a tile group
+    p.finish = (int64_t)n * group * (per_group - 1) <= 64 ? 0 : 2;
+  } else {
+    p.finish = opt.finish == MOAT_FINISH_SECOND_KERNEL ? 2 : 0;
+  }
+  p.front = 3;
+  // the partials follow the fixed counter block, which other calls sharing
+  // the workspace rely on staying zero
+  const bool shared = moat::gemm_groups_shared(groups, rounds, p.splits);
+  p.counter_bytes = shared ? kCounterBlockBytes : 0;
+  p.workspace_bytes = shared ? p.counter_bytes + (int64_t)2 * p.splits * group * n * 256 * (int64_t)sizeof(float) : 0;
+}
+
 GemmPlan plan_gemm(int32_t n, int32_t k, int32_t m, const moat_int4_gemm_options* o) {
   moat_int4_gemm_options opt = {0, 0, 0, 0, 0, 0, 0};
   if (o) opt = *o;
@@ -99,82 +178,12 @@ GemmPlan plan_gemm(int32_t n, int32_t k, int32_t m, const moat_int4_gemm_options
   if (records) {
     // Record-stream kernel.  Tiles per workgroup: 1 (its 4 waves split K four
     // ways), measured fastest at every benchmark shape but the largest, where
-    // 2 ties.  Workgroups: a multiple of the tile-group count (so that the
-    // workgroups of neighbouring groups read the same rows at the same time
-    // and share 128-byte lines in L2), about 2 rounds per wave, at most 512
-    // (2 per CU), and a K split whose fp32 partials stay well below the
-    // weight stream.
+    // 2 ties.
     const int group = opt.group ? opt.group : 1;
     // 8 waves per workgroup only up to 16 rows (the accumulators of 32 rows
     // need more registers than 8 waves leave a lane)
     const int waves = (opt.waves && n <= 16) ? opt.waves : 4;
-    const int groups = moat::gemm_records_groups(m, group);
-    const int64_t tiles_r = moat::gemm_records_tiles(m);
-    // ring depth (LDS: waves x depth x 7 or 8 KB; the launch clamps it to the LDS)
-    const int depth = opt.batch ? opt.batch : (waves == 8 ? 2 : (n <= 16 ? 3 : 2));
-    int64_t splits;
-    if (opt.splits > 0) {
-      splits = opt.splits;
-    } else {
-      // about 8 rounds per workgroup: 2 per wave with 4 waves, 1 with 8
-      splits = (tiles_r * rounds / 8 + groups / 2) / groups;
-      if (splits > 8) splits = 8;  // beyond 8 the hand-off costs more than the shorter loop saves
-      // no more workgroups than the 256 CUs hold at once (a second wave of
-      // workgroups would double the time): one per CU, as the kernel's
-      // registers (over 128 per lane) leave room for one wave per SIMD with 4
-      // waves per workgroup, two with 8
-      const int64_t resident = 256;
-      const int64_t cap_wgs = resident / groups > 0 ? resident / groups : 1;
-      if (splits > cap_wgs) splits = cap_wgs;
-      // above 16 rows the partial sums (N x 256 floats per workgroup) weigh:
-      // stop at about one workgroup per CU
-      if (n > 16) {
-        const int64_t one_per_cu = 256 / groups > 2 ? 256 / groups : 2;
-        if (splits > one_per_cu) splits = one_per_cu;
-      }
-      int64_t by_traffic = k / (16 * n);
-      if (by_traffic < 2) by_traffic = 2;
-      if (splits > by_traffic) splits = by_traffic;
-      if (splits < 1) splits = 1;
-      // prefer a count that divides the rounds: every workgroup then holds
-      // one segment of one tile group (a range that crosses a group boundary
-      // costs a second segment, measured ~3 us per call)
-      for (int64_t s = splits; s * 2 >= splits; --s) {
-        if (rounds % s == 0) {
-          splits = s;
-          break;
-        }
-      }
-    }
-    int64_t wgs = (int64_t)groups * splits;
-    const int64_t items = (int64_t)groups * rounds;
-    if (wgs > items) wgs = items;
-    // the kernel addresses the partials with 32-bit byte offsets
-    const int64_t max_wgs = (int64_t)0xFFFFFFFF / ((int64_t)2 * group * n * 256 * (int64_t)sizeof(float));
-    if (wgs > max_wgs) wgs = max_wgs;
-    p.splits = (int)wgs;
-    p.group = group;
-    p.waves = waves;
-    p.batch = depth;
-    // shared tile groups: summed in the kernel by the workgroup that owns the
-    // group (MOAT_FINISH_DEVICE_ATOMICS or MOAT_FINISH_FENCES) or by a fix-up
-    // kernel (MOAT_FINISH_SECOND_KERNEL).  Automatic: in the kernel while the
-    // owner reads at most 64 KB of partials (n x 1 KB per tile and
-    // contributor), which saves the second launch; beyond that the owner's
-    // one CU is slower than the fix-up kernel spread over many.
-    if (opt.finish == MOAT_FINISH_AUTO) {
-      const int64_t per_group = (wgs + groups - 1) / groups;  // workgroups sharing a tile group
-      p.finish = (int64_t)n * group * (per_group - 1) <= 64 ? 0 : 2;
-    } else {
-      p.finish = opt.finish == MOAT_FINISH_SECOND_KERNEL ? 2 : 0;
-    }
-    p.front = 3;
-    // the partials follow the fixed counter block, which other calls sharing
-    // the workspace rely on staying zero
-    const bool shared = moat::gemm_records_shares_tiles(k, m, group, p.splits);
-    p.counter_bytes = shared ? kCounterBlockBytes : 0;
-    p.workspace_bytes =
-        shared ? p.counter_bytes + (int64_t)2 * p.splits * group * n * 256 * (int64_t)sizeof(float) : 0;
+    plan_records(p, n, k, moat::gemm_records_groups(m, group), moat::gemm_records_tiles(m), group, waves, opt);
     return p;
   }
   const int tiles = moat::gemm_col_tiles(m);
@@ -208,6 +217,38 @@ GemmPlan plan_gemm(int32_t n, int32_t k, int32_t m, const moat_int4_gemm_options
     p.workspace_bytes = 0;
   }
   return p;
+}
+
+// Fused launches (the kernel's RecMode values).
+constexpr int kFusedMulti = 1;
+constexpr int kFusedSwiglu = 2;
+constexpr int kMaxFusedMats = 4;
+
+bool fused_shape_ok(int32_t count, int32_t n, int32_t k, int32_t m) {
+  return count >= 1 && count <= kMaxFusedMats && gemm_shape_ok(n, k, m) && moat::gemm_records_eligible(k, m);
+}
+
+GemmPlan plan_fused(int mode, int32_t count, int32_t n, int32_t k, int32_t m) {
+  GemmPlan p = {};
+  const moat_int4_gemm_options opt = {0, 0, 0, 0, 0, 0, 0};
+  const int64_t tiles = moat::gemm_records_tiles(m);
+  const int group = mode == kFusedSwiglu ? 2 : 1;  // SwiGLU: a gate tile and an up tile per group
+  plan_records(p, n, k, moat::gemm_fused_groups(mode, count, m), (mode == kFusedSwiglu ? 2 : count) * tiles, group,
+               4, opt);
+  p.algo = MOAT_GEMM_MFMA;
+  return p;
+}
+
+int32_t run_fused(int mode, const uint16_t* x, const uint8_t* const* sbs, float* const* ys, uint16_t* h, int32_t count,
+                  int32_t n, int32_t k, int32_t m, void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+  const GemmPlan p = plan_fused(mode, count, n, k, m);
+  float* partials = nullptr;
+  if (p.workspace_bytes > 0) {
+    if (!workspace || workspace_bytes < p.workspace_bytes || !aligned(workspace, 16)) return MOAT_ERR_WORKSPACE;
+    partials = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + p.counter_bytes);
+  }
+  return status_of(moat::launch_gemm_fused(mode, x, sbs, ys, h, count, n, k, m, p.splits, p.batch, p.finish,
+                                           partials, stream));
 }
 
 }  // namespace
@@ -264,6 +305,38 @@ int32_t moat_int4_gemm_ex(const uint16_t* x_f16, const uint8_t* superblocks, flo
 int32_t moat_int4_gemm(const uint16_t* x_f16, const uint8_t* superblocks, float* y_f32, int32_t n, int32_t k,
                        int32_t m, void* workspace, int64_t workspace_bytes, hipStream_t stream) {
   return moat_int4_gemm_ex(x_f16, superblocks, y_f32, n, k, m, nullptr, workspace, workspace_bytes, stream);
+}
+
+int64_t moat_int4_gemm_multi_workspace_size(int32_t count, int32_t n, int32_t k, int32_t m) {
+  if (!fused_shape_ok(count, n, k, m)) return -1;
+  return plan_fused(kFusedMulti, count, n, k, m).workspace_bytes;
+}
+
+int32_t moat_int4_gemm_multi(const uint16_t* x_f16, const uint8_t* const* superblocks, float* const* y_f32,
+                             int32_t count, int32_t n, int32_t k, int32_t m, void* workspace, int64_t workspace_bytes,
+                             hipStream_t stream) {
+  if (!fused_shape_ok(count, n, k, m) || !x_f16 || !superblocks || !y_f32 || !aligned(x_f16, 16))
+    return MOAT_ERR_INVALID;
+  for (int i = 0; i < count; ++i) {
+    if (!superblocks[i] || !y_f32[i] || !aligned(superblocks[i], 16) || !aligned(y_f32[i], 4)) return MOAT_ERR_INVALID;
+  }
+  return run_fused(kFusedMulti, x_f16, superblocks, y_f32, nullptr, count, n, k, m, workspace, workspace_bytes,
+                   stream);
+}
+
+int64_t moat_int4_gemm_swiglu_workspace_size(int32_t n, int32_t k, int32_t m) {
+  if (!fused_shape_ok(2, n, k, m)) return -1;
+  return plan_fused(kFusedSwiglu, 2, n, k, m).workspace_bytes;
+}
+
+int32_t moat_int4_gemm_swiglu(const uint16_t* x_f16, const uint8_t* gate_superblocks, const uint8_t* up_superblocks,
+                              uint16_t* h_f16, int32_t n, int32_t k, int32_t m, void* workspace,
+                              int64_t workspace_bytes, hipStream_t stream) {
+  if (!fused_shape_ok(2, n, k, m) || !x_f16 || !gate_superblocks || !up_superblocks || !h_f16) return MOAT_ERR_INVALID;
+  if (!aligned(x_f16, 16) || !aligned(gate_superblocks, 16) || !aligned(up_superblocks, 16) || !aligned(h_f16, 8))
+    return MOAT_ERR_INVALID;
+  const uint8_t* sbs[2] = {gate_superblocks, up_superblocks};
+  return run_fused(kFusedSwiglu, x_f16, sbs, nullptr, h_f16, 2, n, k, m, workspace, workspace_bytes, stream);
 }
 
 int32_t moat_int4_workspace_clear(void* workspace, int64_t bytes, hipStream_t stream) {

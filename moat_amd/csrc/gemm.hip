@@ -85,7 +85,42 @@ struct GemmParams {
   int y_vec;               // y and the partials are 16-byte aligned and m % 4 == 0: float4 stores
   int items_base;          // records kernel (stream-K): workgroup p covers items (tile * rounds + round)
   int items_rem;           //   [p*base + min(p, rem), +base + (p < rem))
+  // Record-stream kernel over several matrices of one shape that share X:
+  // kModeMulti: tile t of the concatenated tile space is tile t - i*tiles of
+  // matrix i = t / tiles (Y_i = X @ W_i); kModeSwiglu: tile group g pairs tile
+  // g of matrix 0 (gate) with tile g of matrix 1 (up), and the output is
+  // h = silu(X @ W_0) * (X @ W_1) in fp16.
+  int mats;
+  const uint8_t* sbm[4];
+  float* ym[4];
+  uint16_t* h;
 };
+
+enum RecMode : int { kModeSingle = 0, kModeMulti = 1, kModeSwiglu = 2 };
+
+// Uniform 4-way select (scalar compares, no indexed access to the arguments).
+template <typename T>
+__device__ __forceinline__ T select4(int i, T a0, T a1, T a2, T a3) {
+  return i == 0 ? a0 : (i == 1 ? a1 : (i == 2 ? a2 : a3));
+}
+
+// SwiGLU of the two projections: silu(g) * u = g / (1 + e^-g) * u in fp32
+// (as the reference's silu_elementwise_mul_kernel), then fp16.  The empty asm
+// keeps the fp32 product a value of its own: without it the compiler fuses
+// the multiply into the fp16 conversion (v_fma_mix), one rounding where the
+// reference has two.
+__device__ __forceinline__ uint2 swiglu4(float4_t g, float4_t u) {
+  uint32_t o[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    float a = g[2 * i] / (1.0f + expf(-g[2 * i])) * u[2 * i];
+    float b = g[2 * i + 1] / (1.0f + expf(-g[2 * i + 1])) * u[2 * i + 1];
+    asm volatile("" : "+v"(a), "+v"(b));
+    const _Float16 ha = (_Float16)a, hb = (_Float16)b;
+    o[i] = (uint32_t)__builtin_bit_cast(uint16_t, ha) | ((uint32_t)__builtin_bit_cast(uint16_t, hb) << 16);
+  }
+  return uint2{o[0], o[1]};
+}
 
 // Round range of split s (no device-side division).
 __device__ __forceinline__ void split_rounds(const GemmParams& P, int split, int& r_begin, int& r_end) {
@@ -823,37 +858,76 @@ __device__ __forceinline__ void store_sc1_at(float* base, uint32_t o, float4_t v
   asm volatile("global_store_dwordx4 %0, %1, %2 sc1" : : "v"(o), "v"(v), "s"(base) : "memory");
 }
 
-// Output of a tile group: tile tl of the group sums `nslots` LDS slots
-// (slot s of tile tl at red + (tl * nslots + s) * per_slot) and goes to Y
-// (part == nullptr) or to the partial slot part + tl * per_slot, plain (for
-// the fix-up kernel) or encoded and device-coherent (for the owner of the
-// group).  The whole workgroup stores, one 4-column quad per thread and step.
-template <int kC, int kW>
-__device__ __forceinline__ void rec_store(const GemmParams& P, const float* red, int per_slot, int nslots, int tg,
-                                          float* part, bool coherent) {
+// Where a tile group's results go: tile tl of the group covers columns
+// m0 + tl*256 .. of `y` (single matrix: adjacent tiles; several matrices: one
+// tile of matrix i); with SwiGLU both tiles (gate, up) cover columns m0 ..
+// and the group writes h.
+struct RecOut {
+  float* y;
+  int m0;
+};
+
+template <int kMode>
+__device__ __forceinline__ int rec_col(const RecOut& o, int tl, int qd) {
+  return o.m0 + (kMode == kModeSwiglu ? 0 : tl * kRecCols) + 4 * qd;
+}
+
+template <int kMode>
+__device__ __forceinline__ void rec_put_y(const GemmParams& P, const RecOut& o, int row, int col, float4_t v) {
+  float* yp = o.y + (int64_t)row * P.m + col;
+  if (P.y_vec) {
+    *reinterpret_cast<float4_t*>(yp) = v;
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) yp[e] = v[e];
+  }
+}
+
+__device__ __forceinline__ void rec_put_h(const GemmParams& P, int row, int col, float4_t g, float4_t u) {
+  *reinterpret_cast<uint2*>(P.h + (int64_t)row * P.m + col) = swiglu4(g, u);  // m % 128 == 0: 8-byte aligned
+}
+
+// Sum of the `nslots` LDS slots of tile tl at quad (row, qd) (slot s of tile tl
+// at red + (tl * nslots + s) * per_slot), in wave order.
+__device__ __forceinline__ float4_t rec_lds_sum(const float* red, int per_slot, int nslots, int tl, int row, int qd) {
+  const float* base = red + tl * nslots * per_slot + red_pos(row, qd >> 2, qd & 3);
+  float4_t v = *reinterpret_cast<const float4_t*>(base);
+  for (int sl = 1; sl < nslots; ++sl) v += *reinterpret_cast<const float4_t*>(base + sl * per_slot);
+  return v;
+}
+
+// Output of a tile group: tile tl of the group sums its LDS slots and goes to
+// Y (part == nullptr; with SwiGLU the two tiles' sums combine into h) or to
+// the partial slot part + tl * per_slot, plain (for the fix-up kernel) or
+// encoded and device-coherent (for the owner of the group).  The whole
+// workgroup stores, one 4-column quad per thread and step.
+template <int kC, int kW, int kMode>
+__device__ __forceinline__ void rec_store(const GemmParams& P, const float* red, int per_slot, int nslots,
+                                          const RecOut& o, float* part, bool coherent) {
+  if (kMode == kModeSwiglu && !part) {
+    for (int idx = threadIdx.x; idx < P.n * 64; idx += kW * 64) {
+      const int row = idx >> 6, qd = idx & 63;
+      const int col = rec_col<kMode>(o, 0, qd);
+      if (col >= P.m) continue;
+      rec_put_h(P, row, col, rec_lds_sum(red, per_slot, nslots, 0, row, qd),
+                rec_lds_sum(red, per_slot, nslots, 1, row, qd));
+    }
+    return;
+  }
   const int total = kC * P.n * 64;
   for (int idx = threadIdx.x; idx < total; idx += kW * 64) {
     const int tl = kC == 1 ? 0 : idx / (P.n * 64);
     const int w = idx - tl * P.n * 64;
     const int row = w >> 6, qd = w & 63;
-    const int tile = tg * kC + tl;
-    const int m0 = tile * kRecCols;
-    if (m0 + 4 * qd >= P.m) continue;
-    const float* base = red + tl * nslots * per_slot + red_pos(row, qd >> 2, qd & 3);
-    float4_t v = *reinterpret_cast<const float4_t*>(base);
-    for (int sl = 1; sl < nslots; ++sl) v += *reinterpret_cast<const float4_t*>(base + sl * per_slot);
+    const int col = rec_col<kMode>(o, tl, qd);
+    if (col >= P.m) continue;
+    const float4_t v = rec_lds_sum(red, per_slot, nslots, tl, row, qd);
     if (part) {
       float* pp = part + tl * per_slot + row * kRecCols + 4 * qd;
       if (coherent) store_sc1(pp, enc_partial(v));
       else *reinterpret_cast<float4_t*>(pp) = v;
     } else {
-      float* yp = P.y + (int64_t)row * P.m + m0 + 4 * qd;
-      if (P.y_vec) {
-        *reinterpret_cast<float4_t*>(yp) = v;
-      } else {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) yp[e] = v[e];
-      }
+      rec_put_y<kMode>(P, o, row, col, v);
     }
   }
 }
@@ -869,9 +943,9 @@ __device__ __forceinline__ void rec_store(const GemmParams& P, const float* red,
 //
 // A thread takes kQ of its quads at a time and kCB contributors of each: the
 // kQ * kCB = 16 loads go out together, one memory round trip per batch.
-template <int kQ, int kCB, int kC, int kW>
-__device__ __forceinline__ void rec_gather_batched(const GemmParams& P, const float* red, int per_slot, int nslots,
-                                                   int tg, int owner, int p0, int& polls) {
+template <int kQ, int kCB, int kC, int kW, int kMode>
+__device__ __forceinline__ void rec_gather_batched(const GemmParams& P, float* red, int per_slot, int nslots,
+                                                   int tg, const RecOut& o, int owner, int p0, int& polls) {
   static_assert(kQ * kCB == 16, "one batch is 16 loads");
   const int item0 = tg * P.rounds;
   const int total = kC * P.n * 64;
@@ -886,7 +960,7 @@ __device__ __forceinline__ void rec_gather_batched(const GemmParams& P, const fl
       const int tl = kC == 1 ? 0 : idx / (P.n * 64);
       const int w = idx - tl * P.n * 64;
       const int row = w >> 6, qd = w & 63;
-      ok[j] = idx < total && (tg * kC + tl) * kRecCols + 4 * qd < P.m;
+      ok[j] = idx < total && rec_col<kMode>(o, tl, qd) < P.m;
       off[j] = ok[j] ? (uint32_t)(4 * (tl * per_slot + row * kRecCols + 4 * qd)) : 0u;  // outside: a harmless read
     }
     float4_t v[kQ];
@@ -936,16 +1010,13 @@ __device__ __forceinline__ void rec_gather_batched(const GemmParams& P, const fl
       const int tl = kC == 1 ? 0 : idx / (P.n * 64);
       const int w = idx - tl * P.n * 64;
       const int row = w >> 6, qd = w & 63;
-      const float* base = red + tl * nslots * per_slot + red_pos(row, qd >> 2, qd & 3);
-      float4_t own = *reinterpret_cast<const float4_t*>(base);
-      for (int sl = 1; sl < nslots; ++sl) own += *reinterpret_cast<const float4_t*>(base + sl * per_slot);
-      v[j] += own;
-      float* yp = P.y + (int64_t)row * P.m + (tg * kC + tl) * kRecCols + 4 * qd;
-      if (P.y_vec) {
-        *reinterpret_cast<float4_t*>(yp) = v[j];
+      v[j] += rec_lds_sum(red, per_slot, nslots, tl, row, qd);
+      if (kMode == kModeSwiglu) {
+        // the group's sum of tile tl replaces its first LDS slot; h follows
+        // once both tiles are summed
+        *reinterpret_cast<float4_t*>(red + tl * nslots * per_slot + red_pos(row, qd >> 2, qd & 3)) = v[j];
       } else {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) yp[e] = v[j][e];
+        rec_put_y<kMode>(P, o, row, rec_col<kMode>(o, tl, qd), v[j]);
       }
     }
   }
@@ -953,20 +1024,35 @@ __device__ __forceinline__ void rec_gather_batched(const GemmParams& P, const fl
 
 // Batch shape by contributor count: as many of a thread's quads per batch as
 // 16 loads allow with every contributor (up to 8) in it.
-template <int kC, int kW>
-__device__ __forceinline__ void rec_gather(const GemmParams& P, const float* red, int per_slot, int nslots, int tg,
-                                           int owner) {
+template <int kC, int kW, int kMode>
+__device__ __forceinline__ void rec_gather(const GemmParams& P, float* red, int per_slot, int nslots, int tg,
+                                           const RecOut& o, int owner) {
   const int p0 = streamk_owner(P, tg * P.rounds);
   int polls = kMaxPolls;  // this thread's budget of repeated loads
   const int contributors = owner - p0;
-  if (contributors <= 2) rec_gather_batched<8, 2, kC, kW>(P, red, per_slot, nslots, tg, owner, p0, polls);
-  else if (contributors <= 4) rec_gather_batched<4, 4, kC, kW>(P, red, per_slot, nslots, tg, owner, p0, polls);
-  else rec_gather_batched<2, 8, kC, kW>(P, red, per_slot, nslots, tg, owner, p0, polls);
+  if (contributors <= 2)
+    rec_gather_batched<8, 2, kC, kW, kMode>(P, red, per_slot, nslots, tg, o, owner, p0, polls);
+  else if (contributors <= 4)
+    rec_gather_batched<4, 4, kC, kW, kMode>(P, red, per_slot, nslots, tg, o, owner, p0, polls);
+  else
+    rec_gather_batched<2, 8, kC, kW, kMode>(P, red, per_slot, nslots, tg, o, owner, p0, polls);
+  if (kMode == kModeSwiglu) {
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < P.n * 64; idx += kW * 64) {
+      const int row = idx >> 6, qd = idx & 63;
+      const int col = rec_col<kMode>(o, 0, qd);
+      if (col >= P.m) continue;
+      rec_put_h(P, row, col, *reinterpret_cast<const float4_t*>(red + red_pos(row, qd >> 2, qd & 3)),
+                *reinterpret_cast<const float4_t*>(red + nslots * per_slot + red_pos(row, qd >> 2, qd & 3)));
+    }
+  }
 }
 
-template <int NR, int kDepth, int kC, int kW>
+template <int NR, int kDepth, int kC, int kW, int kMode>
 __global__ void __launch_bounds__(kW * 64) int4_gemm_records_kernel(GemmParams P) {
   using G = RecGeom<NR>;
+  static_assert(kMode == kModeSingle || (kMode == kModeMulti && kC == 1) || (kMode == kModeSwiglu && kC == 2),
+                "several matrices: one tile per group; SwiGLU: gate and up tile per group");
   constexpr int kShare = kW / kC;  // waves per tile
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   // fetch every argument now, in one batch of scalar loads, rather than at
@@ -974,6 +1060,9 @@ __global__ void __launch_bounds__(kW * 64) int4_gemm_records_kernel(GemmParams P
   asm volatile("" : : "s"(P.x), "s"(P.sb), "s"(P.y), "s"(P.partials), "s"(P.n), "s"(P.k), "s"(P.m),
                "s"(P.rounds), "s"(P.shift), "s"(P.y_vec), "s"(P.items_base), "s"(P.items_rem), "s"(P.tiles),
                "s"(P.finish), "s"(P.splits));
+  if (kMode != kModeSingle)
+    asm volatile("" : : "s"(P.sbm[0]), "s"(P.sbm[1]), "s"(P.sbm[2]), "s"(P.sbm[3]), "s"(P.ym[0]), "s"(P.ym[1]),
+                 "s"(P.ym[2]), "s"(P.ym[3]), "s"(P.h));
   const int lane = threadIdx.x & 63;
   // wave index as a scalar: the round loop below is then uniform control flow
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1036,14 +1125,35 @@ __global__ void __launch_bounds__(kW * 64) int4_gemm_records_kernel(GemmParams P
     const int seg_lo = max(lo, tg * P.rounds);
     const int r0 = seg_lo - tg * P.rounds;
     const int r1 = seg_hi - tg * P.rounds;
-    const int tile = tg * kC + tl;
-    const bool has_tile = tile < P.tiles;  // the last group may be short
-    const int groups = has_tile ? min(8, (P.m - kRecCols * tile) >> 5) : 0;  // 4 or 8 (M % 128 == 0)
+    // this wave's tile: its matrix, its index in that matrix, its records
+    int mat = 0, ltile = tg * kC + tl;
+    if (kMode == kModeMulti) {
+      mat = (ltile >= P.tiles) + (ltile >= 2 * P.tiles) + (ltile >= 3 * P.tiles);
+      ltile -= mat * P.tiles;
+    } else if (kMode == kModeSwiglu) {
+      mat = tl;
+      ltile = tg;
+    }
+    const bool has_tile = ltile < P.tiles && mat < (kMode == kModeSingle ? 1 : P.mats);  // the last group may be short
+    const int groups = has_tile ? min(8, (P.m - kRecCols * ltile) >> 5) : 0;  // 4 or 8 (M % 128 == 0)
     const uint32_t smask = g < groups ? 0xFFFFFFFFu : 0u;
     uint32_t woff[kRecWeightLoads];
 #pragma unroll
     for (int i = 0; i < kRecWeightLoads; ++i) woff[i] = groups < 8 ? slots.half[i] : slots.full[i];
-    const uint8_t* wtile = P.sb + (uint64_t)kSbBytes * (has_tile ? tile : 0);
+    const uint8_t* wmat = kMode == kModeSingle ? P.sb : select4(mat, P.sbm[0], P.sbm[1], P.sbm[2], P.sbm[3]);
+    const uint8_t* wtile = wmat + (uint64_t)kSbBytes * (has_tile ? ltile : 0);
+    // where the group's results go (the group's first tile)
+    RecOut out;
+    if (kMode == kModeSingle) {
+      out.y = P.y;
+      out.m0 = tg * kC * kRecCols;
+    } else if (kMode == kModeMulti) {
+      out.y = select4(mat, P.ym[0], P.ym[1], P.ym[2], P.ym[3]);
+      out.m0 = ltile * kRecCols;
+    } else {
+      out.y = nullptr;
+      out.m0 = tg * kRecCols;
+    }
 
     RecAcc<NR> acc;
 #pragma unroll
@@ -1103,54 +1213,80 @@ __global__ void __launch_bounds__(kW * 64) int4_gemm_records_kernel(GemmParams P
     const int pslot = 2 * p + (seg_lo == lo ? 0 : 1);
     const bool in_kernel = P.finish != kFinishSecondKernel;
     if (!whole && in_kernel && r1 == P.rounds) {
-      rec_gather<kC, kW>(P, red, per_slot, kSlots, tg, p);  // this workgroup owns the group
+      rec_gather<kC, kW, kMode>(P, red, per_slot, kSlots, tg, out, p);  // this workgroup owns the group
     } else {
-      rec_store<kC, kW>(P, red, per_slot, kSlots, tg,
-                        whole ? nullptr : P.partials + (int64_t)pslot * kC * per_slot, in_kernel);
+      rec_store<kC, kW, kMode>(P, red, per_slot, kSlots, out,
+                               whole ? nullptr : P.partials + (int64_t)pslot * kC * per_slot, in_kernel);
     }
     __syncthreads();  // LDS is the next segment's ring
     seg_hi = seg_lo;
   }
 }
 
-// Fix-up of the tile groups that several workgroups share: Y = sum of their
-// partials in workgroup order.  One thread per 4-column quad of a tile.
-__global__ void __launch_bounds__(256) streamk_fixup_kernel(GemmParams P, int group_tiles) {
-  const int per_tile = P.n * 64;
-  const int total = P.tiles * per_tile;
+// Sum of tile tl's partials of tile group tg at quad (row, qd) over the
+// contributing workgroups p0 .. p1, in workgroup order; the slots are left at
+// zero (the in-kernel hand-off reads zero as empty).  The partials are
+// independent loads: 8 go out before any add (a load-then-add loop would pay
+// one memory round trip per partial).
+__device__ __forceinline__ float4_t fixup_sum(const GemmParams& P, int group_tiles, int item0, int p0, int p1, int tl,
+                                              int row, int qd) {
   const int per_slot = P.n * kRecCols;
+  float4_t v = {0.f, 0.f, 0.f, 0.f};
+  const int64_t off = (int64_t)tl * per_slot + row * kRecCols + 4 * qd;
+  for (int p8 = p0; p8 <= p1; p8 += 8) {
+    float4_t t[8];
+    float4_t* a[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int pp = min(p8 + i, p1);  // past the end: re-read the last one, added as 0 below
+      const int lo_p = pp * P.items_base + min(pp, P.items_rem);
+      const int pslot = 2 * pp + (lo_p < item0 ? 1 : 0);
+      a[i] = reinterpret_cast<float4_t*>(P.partials + (int64_t)pslot * group_tiles * per_slot + off);
+      t[i] = *a[i];
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i)  // in workgroup order
+      if (p8 + i <= p1) v += t[i];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (p8 + i <= p1) *a[i] = float4_t{0.f, 0.f, 0.f, 0.f};
+  }
+  return v;
+}
+
+// Fix-up of the tile groups that several workgroups share: Y = sum of their
+// partials in workgroup order (with SwiGLU, h from the gate and up sums).
+// One thread per 4-column quad of a tile (of a gate/up pair).
+__global__ void __launch_bounds__(256) streamk_fixup_kernel(GemmParams P, int group_tiles, int mode) {
+  const int per_tile = P.n * 64;
+  const int tiles = mode == kModeMulti ? P.mats * P.tiles : P.tiles;  // tiles (gate/up pairs) to cover
+  const int total = tiles * per_tile;
   for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < total; e += gridDim.x * blockDim.x) {
     const int tile = e / per_tile, w = e - tile * per_tile;
     const int row = w >> 6, qd = w & 63;
-    const int m0 = tile * kRecCols;
-    if (m0 + 4 * qd >= P.m) continue;
-    const int tg = tile / group_tiles, tl = tile - tg * group_tiles;
+    const int tg = mode == kModeSwiglu ? tile : tile / group_tiles;
     const int item0 = tg * P.rounds;
     const int p0 = streamk_owner(P, item0), p1 = streamk_owner(P, item0 + P.rounds - 1);
-    if (p0 == p1) continue;  // one workgroup covered the group and wrote Y
-    // the partials are independent loads: issue 8 before adding any (a
-    // load-then-add loop would pay one memory round trip per partial)
-    float4_t v = {0.f, 0.f, 0.f, 0.f};
-    const int64_t off = (int64_t)tl * per_slot + row * kRecCols + 4 * qd;
-    for (int p8 = p0; p8 <= p1; p8 += 8) {
-      float4_t t[8];
-      float4_t* a[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int pp = min(p8 + i, p1);  // past the end: re-read the last one, added as 0 below
-        const int lo_p = pp * P.items_base + min(pp, P.items_rem);
-        const int pslot = 2 * pp + (lo_p < item0 ? 1 : 0);
-        a[i] = reinterpret_cast<float4_t*>(P.partials + (int64_t)pslot * group_tiles * per_slot + off);
-        t[i] = *a[i];
-      }
-#pragma unroll
-      for (int i = 0; i < 8; ++i)  // in workgroup order
-        if (p8 + i <= p1) v += t[i];
-#pragma unroll
-      for (int i = 0; i < 8; ++i)  // leave the slots at zero (the in-kernel hand-off reads zero as empty)
-        if (p8 + i <= p1) *a[i] = float4_t{0.f, 0.f, 0.f, 0.f};
+    if (p0 == p1) continue;  // one workgroup covered the group and wrote it
+    if (mode == kModeSwiglu) {
+      const int col = tile * kRecCols + 4 * qd;
+      if (col >= P.m) continue;
+      const float4_t gsum = fixup_sum(P, 2, item0, p0, p1, 0, row, qd);
+      const float4_t usum = fixup_sum(P, 2, item0, p0, p1, 1, row, qd);
+      *reinterpret_cast<uint2*>(P.h + (int64_t)row * P.m + col) = swiglu4(gsum, usum);
+      continue;
     }
-    float* yp = P.y + (int64_t)row * P.m + m0 + 4 * qd;
+    const int tl = tile - tg * group_tiles;
+    int mat = 0, ltile = tile;
+    if (mode == kModeMulti) {
+      mat = (tile >= P.tiles) + (tile >= 2 * P.tiles) + (tile >= 3 * P.tiles);
+      ltile = tile - mat * P.tiles;
+    }
+    const int col = ltile * kRecCols + 4 * qd;
+    if (col >= P.m) continue;
+    const float4_t v = fixup_sum(P, group_tiles, item0, p0, p1, tl, row, qd);
+    float* yp = (mode == kModeMulti ? select4(mat, P.ym[0], P.ym[1], P.ym[2], P.ym[3]) : P.y) +
+                (int64_t)row * P.m + col;
     if (P.y_vec) {
       *reinterpret_cast<float4_t*>(yp) = v;
     } else {
@@ -1229,12 +1365,12 @@ static hipError_t launch_front(const GemmParams& P, int algo, int batch, hipStre
 // Reduction slots of one tile: one per wave that shares it.
 constexpr int rec_slots_per_tile(int waves, int group_tiles) { return waves / group_tiles; }
 
-template <int NR, int kDepth, int kC, int kW>
+template <int NR, int kDepth, int kC, int kW, int kMode>
 static hipError_t launch_records_one(const GemmParams& P, int wgs, hipStream_t stream) {
   const size_t ring = (size_t)kW * kDepth * RecGeom<NR>::kStageBytes;
   const size_t red = (size_t)kC * rec_slots_per_tile(kW, kC) * P.n * kRecCols * sizeof(float);
   if (ring > kMaxDynamicLds || red > kMaxDynamicLds) return hipErrorInvalidValue;  // never launch past the LDS
-  hipLaunchKernelGGL((int4_gemm_records_kernel<NR, kDepth, kC, kW>), dim3(wgs), dim3(kW * 64),
+  hipLaunchKernelGGL((int4_gemm_records_kernel<NR, kDepth, kC, kW, kMode>), dim3(wgs), dim3(kW * 64),
                      ring > red ? ring : red, stream, P);
   return hipGetLastError();
 }
@@ -1244,11 +1380,11 @@ static hipError_t launch_records_depth(const GemmParams& P, int wgs, int depth, 
   // the ring must fit: clamp the depth (kW waves x depth stages)
   const int max_depth = (int)(kMaxDynamicLds / ((size_t)kW * RecGeom<NR>::kStageBytes));
   if (depth > max_depth) depth = max_depth;
-  if (depth >= 5) return launch_records_one<NR, 5, kC, kW>(P, wgs, stream);
-  if (depth == 4) return launch_records_one<NR, 4, kC, kW>(P, wgs, stream);
-  if (depth == 3) return launch_records_one<NR, 3, kC, kW>(P, wgs, stream);
-  if (depth == 2) return launch_records_one<NR, 2, kC, kW>(P, wgs, stream);
-  return launch_records_one<NR, 1, kC, kW>(P, wgs, stream);
+  if (depth >= 5) return launch_records_one<NR, 5, kC, kW, kModeSingle>(P, wgs, stream);
+  if (depth == 4) return launch_records_one<NR, 4, kC, kW, kModeSingle>(P, wgs, stream);
+  if (depth == 3) return launch_records_one<NR, 3, kC, kW, kModeSingle>(P, wgs, stream);
+  if (depth == 2) return launch_records_one<NR, 2, kC, kW, kModeSingle>(P, wgs, stream);
+  return launch_records_one<NR, 1, kC, kW, kModeSingle>(P, wgs, stream);
 }
 
 template <int NR, int kW>
@@ -1268,6 +1404,15 @@ static hipError_t launch_records(const GemmParams& P, int wgs, int depth, int gr
   return launch_records_group<NR, 4>(P, wgs, depth, group_tiles, stream);
 }
 
+// Several matrices (one tile per group) or SwiGLU pairs (gate and up tile per
+// group): 4 waves, ring depth 2 or 3.
+template <int NR, int kMode>
+static hipError_t launch_records_fused(const GemmParams& P, int wgs, int depth, hipStream_t stream) {
+  constexpr int kC = kMode == kModeSwiglu ? 2 : 1;
+  if (depth >= 3) return launch_records_one<NR, 3, kC, 4, kMode>(P, wgs, stream);
+  return launch_records_one<NR, 2, kC, 4, kMode>(P, wgs, stream);
+}
+
 bool gemm_records_eligible(int k, int m) { return (m % 128) == 0 && (k % kRoundRows) == 0; }
 
 // Dynamic LDS of one record-stream workgroup (after the depth clamp).
@@ -1276,17 +1421,30 @@ int gemm_records_groups(int m, int group_tiles) { return (gemm_records_tiles(m) 
 
 // Workgroups of a stream-K launch share tile groups unless every range is a
 // whole number of groups.
-bool gemm_records_shares_tiles(int k, int m, int group_tiles, int wgs) {
-  const int64_t rounds = k / kRoundRows;
-  const int64_t items = (int64_t)gemm_records_groups(m, group_tiles) * rounds;
+bool gemm_groups_shared(int64_t groups, int64_t rounds, int wgs) {
+  const int64_t items = groups * rounds;
   const int64_t base = items / wgs, rem = items % wgs;
   return !(rem == 0 && base % rounds == 0);
+}
+
+bool gemm_records_shares_tiles(int k, int m, int group_tiles, int wgs) {
+  return gemm_groups_shared(gemm_records_groups(m, group_tiles), k / kRoundRows, wgs);
+}
+
+// Tile groups of a fused launch: `mats` matrices of one tile each per group,
+// or (SwiGLU) one gate/up pair per group.
+int gemm_fused_groups(int mode, int mats, int m) {
+  return mode == kModeSwiglu ? gemm_records_tiles(m) : mats * gemm_records_tiles(m);
+}
+
+bool gemm_fused_shares_tiles(int mode, int mats, int k, int m, int wgs) {
+  return gemm_groups_shared(gemm_fused_groups(mode, mats, m), k / kRoundRows, wgs);
 }
 
 hipError_t launch_gemm(int algo, const uint16_t* x, const uint8_t* sb, float* y, int n, int k, int m, int splits,
                        int batch, int finish, int front, int group, int waves, float* partials, uint32_t* counters,
                        hipStream_t stream) {
-  GemmParams P;
+  GemmParams P = {};
   P.x = x; P.sb = sb; P.y = y; P.partials = partials; P.counters = counters;
   P.n = n; P.k = k; P.m = m; P.splits = splits; P.rounds = gemm_rounds(k); P.tiles = gemm_col_tiles(m);
   P.x_vec = ((reinterpret_cast<uintptr_t>(x) & 15) == 0 && (k % 8) == 0) ? 1 : 0;
@@ -1316,7 +1474,7 @@ hipError_t launch_gemm(int algo, const uint16_t* x, const uint8_t* sb, float* y,
       const int quads = P.tiles * P.n * 64;
       int blocks = (quads + 255) / 256;
       if (blocks > 2048) blocks = 2048;
-      hipLaunchKernelGGL(streamk_fixup_kernel, dim3(blocks), dim3(256), 0, stream, P, group_tiles);
+      hipLaunchKernelGGL(streamk_fixup_kernel, dim3(blocks), dim3(256), 0, stream, P, group_tiles, (int)kModeSingle);
       return hipGetLastError();
     }
     front = kFrontVgprLds;
@@ -1331,6 +1489,48 @@ hipError_t launch_gemm(int algo, const uint16_t* x, const uint8_t* sb, float* y,
   int64_t blocks = (nm + 255) / 256;
   if (blocks > 4096) blocks = 4096;
   hipLaunchKernelGGL(splitk_sum_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, partials, splits, nm, y);
+  return hipGetLastError();
+}
+
+// Record-stream GEMM of `mats` matrices of one shape sharing X (mode
+// kModeMulti: Y_i = X @ W_i) or of a gate/up pair (kModeSwiglu: h =
+// silu(X @ W_0) * (X @ W_1) in fp16).  The caller has checked the shape
+// (m % 128 == 0, k % 32 == 0, x 16-byte aligned).
+hipError_t launch_gemm_fused(int mode, const uint16_t* x, const uint8_t* const* sbs, float* const* ys, uint16_t* h,
+                             int mats, int n, int k, int m, int wgs, int depth, int finish, float* partials,
+                             hipStream_t stream) {
+  GemmParams P = {};
+  P.x = x; P.sb = sbs[0]; P.y = ys ? ys[0] : nullptr; P.partials = partials; P.counters = nullptr;
+  P.n = n; P.k = k; P.m = m; P.splits = wgs; P.rounds = gemm_rounds(k);
+  P.tiles = gemm_records_tiles(m);
+  P.x_vec = 1;
+  P.finish = finish;
+  P.shift = (m % kRecCols) != 0;
+  const int items = gemm_fused_groups(mode, mats, m) * P.rounds;
+  P.items_base = items / wgs;
+  P.items_rem = items % wgs;
+  P.mats = mats;
+  int y_vec = 1;
+  for (int i = 0; i < 4; ++i) {
+    P.sbm[i] = sbs[i < mats ? i : 0];
+    P.ym[i] = ys ? ys[i < mats ? i : 0] : nullptr;
+    if (ys && i < mats && (reinterpret_cast<uintptr_t>(ys[i]) & 15) != 0) y_vec = 0;
+  }
+  P.y_vec = y_vec;
+  P.h = h;
+  hipError_t e;
+  if (mode == kModeSwiglu)
+    e = n <= 16 ? launch_records_fused<1, kModeSwiglu>(P, wgs, depth, stream)
+                : launch_records_fused<2, kModeSwiglu>(P, wgs, depth, stream);
+  else
+    e = n <= 16 ? launch_records_fused<1, kModeMulti>(P, wgs, depth, stream)
+                : launch_records_fused<2, kModeMulti>(P, wgs, depth, stream);
+  if (e != hipSuccess || !gemm_fused_shares_tiles(mode, mats, k, m, wgs) || finish != kFinishSecondKernel) return e;
+  const int tiles = mode == kModeMulti ? mats * P.tiles : P.tiles;
+  const int quads = tiles * n * 64;
+  int blocks = (quads + 255) / 256;
+  if (blocks > 2048) blocks = 2048;
+  hipLaunchKernelGGL(streamk_fixup_kernel, dim3(blocks), dim3(256), 0, stream, P, mode == kModeSwiglu ? 2 : 1, mode);
   return hipGetLastError();
 }
 

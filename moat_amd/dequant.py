@@ -293,6 +293,88 @@ def _gemm_into(x: torch.Tensor, blob: torch.Tensor, y: torch.Tensor, K: int, M: 
                                      D.ptr(ws), ws_bytes, D.stream()), "batched_int4_matmul")
 
 
+def _fused_inputs(x, K: int, M: int, blobs):
+    K, M = int(K), int(M)
+    if K < 1 or K % 32 != 0 or M < 128 or M % 128 != 0:
+        raise ValueError(f"fused projections need K % 32 == 0 and M % 128 == 0 (got K={K}, M={M}); "
+                         "use batched_int4_matmul per matrix")
+    xs = D.to_device(x)
+    if xs.dim() == 1:
+        xs = xs.reshape(1, -1)
+    if xs.dim() != 2 or xs.shape[1] != K:
+        raise ValueError(f"x must be (N, {K}), got {tuple(xs.shape)}")
+    if xs.dtype != torch.float16:
+        xs = xs.to(torch.float16)
+    xs = D.aligned(xs.contiguous(), 16)
+    n_sb = K * M // SUPERBLOCK_ELEMS
+    return xs, [_blob_to_device(b, n_sb) for b in blobs]
+
+
+def batched_int4_matmul_multi(x, superblocks_list, K: int, M: int):
+    """``[f32(X) @ f32(deq(W_i)) for W_i in superblocks_list]``: 1 to 4
+    matrices of one shape (K x M) that share the activations X, in one launch
+    per 32 rows of X (``moat_int4_gemm_multi``); each result equals
+    :func:`batched_int4_matmul` on that matrix (to float32 summation order).
+    ValueError unless ``K % 32 == 0`` and ``M % 128 == 0``."""
+    want_t = D.is_tensor(x)
+    blobs_in = list(superblocks_list)
+    if not 1 <= len(blobs_in) <= 4:
+        raise ValueError(f"1 to 4 matrices, got {len(blobs_in)}")
+    xs, blobs = _fused_inputs(x, K, M, blobs_in)
+    N = xs.shape[0]
+    ys = [torch.empty((N, M), dtype=torch.float32, device=xs.device) for _ in blobs]
+    for r0 in range(0, N, MAX_BATCH_PER_CALL):
+        r1 = min(N, r0 + MAX_BATCH_PER_CALL)
+        _multi_into(xs[r0:r1], blobs, [y[r0:r1] for y in ys], int(K), int(M))
+    return [D.out_like(y, want_t) for y in ys]
+
+
+def _multi_into(x: torch.Tensor, blobs, ys, K: int, M: int) -> None:
+    """One ``moat_int4_gemm_multi`` launch: x (n <= 32, K) fp16 16-byte
+    aligned, device record streams, (n, M) fp32 outputs."""
+    lib = _lib.load()
+    n, count = x.shape[0], len(blobs)
+    ws_bytes = lib.moat_int4_gemm_multi_workspace_size(count, n, K, M)
+    if ws_bytes < 0:
+        raise ValueError(f"unsupported fused configuration count={count} N={n} K={K} M={M}")
+    ws = D.workspaces.get(ws_bytes)
+    sb_ptrs = (ctypes.c_void_p * count)(*[D.ptr(b) for b in blobs])
+    y_ptrs = (ctypes.c_void_p * count)(*[D.ptr(y) for y in ys])
+    _lib.check(lib.moat_int4_gemm_multi(D.ptr(x), sb_ptrs, y_ptrs, count, n, K, M, D.ptr(ws), ws_bytes, D.stream()),
+               "batched_int4_matmul_multi")
+
+
+def int4_swiglu(x, gate_superblocks, up_superblocks, K: int, M: int):
+    """``h = fp16(silu(g) * u)`` with ``g = f32(X) @ f32(deq(W_gate))``,
+    ``u = f32(X) @ f32(deq(W_up))`` and ``silu(g) = g / (1 + exp(-g))`` in
+    fp32 (antigravity-engine/src/shaders/transformer_ops.metal:216-232 on the
+    two projections of transformer_engine.mm:694-713), in one launch per 32
+    rows of X (``moat_int4_gemm_swiglu``); fp16 (N, M) out, the down
+    projection's input.  ValueError unless ``K % 32 == 0`` and
+    ``M % 128 == 0``."""
+    want_t = D.is_tensor(x)
+    xs, (gb, ub) = _fused_inputs(x, K, M, [gate_superblocks, up_superblocks])
+    N = xs.shape[0]
+    h = torch.empty((N, M), dtype=torch.float16, device=xs.device)
+    for r0 in range(0, N, MAX_BATCH_PER_CALL):
+        r1 = min(N, r0 + MAX_BATCH_PER_CALL)
+        _swiglu_into(xs[r0:r1], gb, ub, h[r0:r1], int(K), int(M))
+    return D.out_like(h, want_t)
+
+
+def _swiglu_into(x: torch.Tensor, gate: torch.Tensor, up: torch.Tensor, h: torch.Tensor, K: int, M: int) -> None:
+    """One ``moat_int4_gemm_swiglu`` launch: x (n <= 32, K) fp16 16-byte
+    aligned, device record streams, (n, M) fp16 output."""
+    lib = _lib.load()
+    n = x.shape[0]
+    ws_bytes = lib.moat_int4_gemm_swiglu_workspace_size(n, K, M)
+    if ws_bytes < 0:
+        raise ValueError(f"unsupported fused configuration N={n} K={K} M={M}")
+    ws = D.workspaces.get(ws_bytes)
+    _lib.check(lib.moat_int4_gemm_swiglu(D.ptr(x), D.ptr(gate), D.ptr(up), D.ptr(h), n, K, M, D.ptr(ws), ws_bytes,
+                                         D.stream()), "int4_swiglu")
+
+
 def batched_int4_matmul(x, superblocks, K: int, M: int, out=None, *, algo: int = _lib.GEMM_AUTO,
                         splits: int = 0, batch: int = 0, finish: int = 0, front: int = 0, group: int = 0,
                         waves: int = 0):

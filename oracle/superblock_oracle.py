@@ -274,6 +274,21 @@ def gemv_stack(x, blob, K: int, M: int) -> np.ndarray:
     return np.vstack([x32[i:i + 1] @ w for i in range(x32.shape[0])])
 
 
+def silu_mul(g, u) -> np.ndarray:
+    """``silu(g) * u = g / (1 + exp(-g)) * u`` in float64: the SwiGLU step of
+    ``antigravity-engine/src/shaders/transformer_ops.metal:216-232`` (which
+    evaluates it in fp32 on fp16 inputs and rounds the result to fp16)."""
+    g = np.asarray(g, dtype=np.float64)
+    return g / (1.0 + np.exp(-g)) * np.asarray(u, dtype=np.float64)
+
+
+def swiglu_ref(x, gate_blob, up_blob, K: int, M: int) -> np.ndarray:
+    """``silu(X @ W_gate) * (X @ W_up)`` (float64) with both projections as
+    :func:`gemm_ref`: the MLP front of ``transformer_engine.mm:694-713`` /
+    ``transformer.py:133-134``."""
+    return silu_mul(gemm_ref(x, gate_blob, K, M), gemm_ref(x, up_blob, K, M))
+
+
 def footprint(num_params: int, group_size: int = GROUP, bits: int = 4) -> dict:
     """Closed forms of ``src/dequant.py:150-187``: 0.5 B/param + 2 B/group."""
     weight_bytes = num_params * (bits / 8.0)

@@ -144,6 +144,49 @@ def test_other_entry_points_validate(lib):
     assert lib.moat_int4_workspace_clear(None, 16, None) == I
 
 
+def test_fused_entry_points_validate(lib):
+    I = _lib.MOAT_ERR_INVALID
+    P2 = ctypes.c_void_p * 2
+    sbs, ys = P2(FAKE.value, FAKE.value), P2(FAKE.value, FAKE.value)
+    # count 1..4, the record-stream kernel's shapes only (m % 128, k % 32)
+    assert lib.moat_int4_gemm_multi_workspace_size(0, 1, 2048, 2048) == -1
+    assert lib.moat_int4_gemm_multi_workspace_size(5, 1, 2048, 2048) == -1
+    assert lib.moat_int4_gemm_multi_workspace_size(2, 1, 2048, 2016) == -1  # m % 128
+    assert lib.moat_int4_gemm_multi_workspace_size(2, 1, 40, 2048) == -1    # k % 32
+    assert lib.moat_int4_gemm_multi_workspace_size(2, 33, 2048, 2048) == -1
+    assert lib.moat_int4_gemm_multi_workspace_size(3, 1, 2048, 2048) >= 0
+    assert lib.moat_int4_gemm_swiglu_workspace_size(1, 2048, 2016) == -1
+    assert lib.moat_int4_gemm_swiglu_workspace_size(16, 2048, 5632) >= 0
+    assert lib.moat_int4_gemm_multi(FAKE, sbs, ys, 2, 1, 2048, 2016, None, 0, None) == I
+    assert lib.moat_int4_gemm_multi(None, sbs, ys, 2, 1, 2048, 2048, None, 0, None) == I
+    assert lib.moat_int4_gemm_multi(FAKE, None, ys, 2, 1, 2048, 2048, None, 0, None) == I
+    assert lib.moat_int4_gemm_multi(FAKE, P2(FAKE.value, None), ys, 2, 1, 2048, 2048, None, 0, None) == I
+    assert lib.moat_int4_gemm_multi(FAKE, P2(FAKE.value, 0x10008), ys, 2, 1, 2048, 2048, None, 0, None) == I
+    assert lib.moat_int4_gemm_multi(ctypes.c_void_p(0x10008), sbs, ys, 2, 1, 2048, 2048, None, 0, None) == I  # x 16 B
+    assert lib.moat_int4_gemm_swiglu(FAKE, FAKE, FAKE, ctypes.c_void_p(0x10004), 1, 2048, 2048, None, 0, None) == I
+    assert lib.moat_int4_gemm_swiglu(FAKE, None, FAKE, FAKE, 1, 2048, 2048, None, 0, None) == I
+    # a shared-tile plan needs the workspace: refused before any launch
+    size = lib.moat_int4_gemm_swiglu_workspace_size(16, 2048, 5632)
+    if size > 0:
+        assert lib.moat_int4_gemm_swiglu(FAKE, FAKE, FAKE, FAKE, 16, 2048, 5632, None, 0, None) == _lib.MOAT_ERR_WORKSPACE
+    size = lib.moat_int4_gemm_multi_workspace_size(3, 1, 2048, 2048)
+    if size > 0:
+        P3 = ctypes.c_void_p * 3
+        assert lib.moat_int4_gemm_multi(FAKE, P3(*[FAKE.value] * 3), P3(*[FAKE.value] * 3), 3, 1, 2048, 2048,
+                                        FAKE, size - 1, None) == _lib.MOAT_ERR_WORKSPACE
+
+
+def test_fused_python_shapes_checked_first():
+    import numpy as np
+    from moat_amd import dequant
+    with pytest.raises(ValueError):
+        dequant.batched_int4_matmul_multi(np.zeros((1, 40), np.float16), [np.zeros(15 * 144, np.uint8)], 40, 96)
+    with pytest.raises(ValueError):
+        dequant.batched_int4_matmul_multi(np.zeros((1, 64), np.float16), [], 64, 128)
+    with pytest.raises(ValueError):
+        dequant.int4_swiglu(np.zeros((1, 64), np.float16), None, None, 64, 96)
+
+
 def test_product_refuses_to_run_without_gpu():
     import torch
     if torch.cuda.is_available():

@@ -309,3 +309,15 @@ def test_footprint_known_answers():
     assert O.footprint(3_000_000_000)["total_gb"] < 2.0
     assert O.footprint(7_000_000_000)["total_gb"] < 4.0
     assert O.footprint(256)["total_bytes"] == 144.0
+
+
+def test_silu_mul_closed_forms():
+    """silu(0) = 0; silu(1) = 1 / (1 + 1/e); silu(-1) = -1 / (1 + e); large |g|:
+    silu(g) -> g (g > 0) and -> 0 (g < 0); the product scales with u."""
+    import math
+    g = np.array([0.0, 1.0, -1.0, 40.0, -40.0, 1.0])
+    u = np.array([5.0, 2.0, 1.0, 0.5, 3.0, -3.0])
+    got = O.silu_mul(g, u)
+    want = [0.0, 2.0 / (1.0 + math.exp(-1.0)), -1.0 / (1.0 + math.e), 20.0, 0.0, -3.0 / (1.0 + math.exp(-1.0))]
+    assert np.allclose(got, want, rtol=1e-15, atol=1e-15)
+    assert abs(got[4]) < 1e-15
