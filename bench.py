@@ -31,12 +31,14 @@ CONFIGS = {
     "k2048_m5504": (2048, 5504, 0.02, 1002, 0.0, [1, 2, 4, 8, 16, 32]),
     "k3072_m8192": (3072, 8192, 0.02, 1003, 0.0, [1, 2, 4, 8, 16, 32]),
     "k8192_m28672": (8192, 28672, 0.01, 1005, 0.001, [1, 32]),
+    "k2048_m32000": (2048, 32000, 0.02, 1006, 0.0, [1, 2, 4, 8, 16, 32]),
 }
 WORKLOAD_NAMES = {
     "k2048_m2048": "int4 superblock projection 2048x2048",
     "k2048_m5504": "int4 superblock FFN gate/up projection K=2048 M=5504, N sweep 1..32",
     "k3072_m8192": "int4 superblock FFN projection K=3072 M=8192, N sweep 1..32",
     "k8192_m28672": "int4 superblock projection K=8192 M=28672 (70B-class FFN, 0.1% 8-sigma outliers)",
+    "k2048_m32000": "int4 superblock LM head K=2048 (hidden) x M=32000 (vocabulary), N sweep 1..32",
 }
 ROTATE_BYTES = 300 * 1024 * 1024
 # One decoder layer's projections at hidden 2048 (Q, K, V, O 2048x2048; gate
@@ -135,8 +137,9 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="k2048_m5504", choices=sorted(CONFIGS) + ["layer_h2048"],
-                    help="projection shape, or layer_h2048: one decoder layer's 7 projections at N=16")
+    ap.add_argument("--config", default="k2048_m5504", choices=sorted(CONFIGS) + ["layer_h2048", "quantize_load"],
+                    help="projection shape; layer_h2048: one decoder layer's 7 projections at N=16; "
+                         "quantize_load: fp16 weights of one layer to INT4 records on the GPU")
     ap.add_argument("--ns", default=None, help="comma-separated N values (default: the config's)")
     ap.add_argument("--algo", type=int, default=0, help="0 auto, 1 dot2, 2 mfma")
     ap.add_argument("--splits", type=int, default=0)
@@ -172,6 +175,8 @@ def main() -> int:
 
     if args.config == "layer_h2048":
         return run_layer(args)
+    if args.config == "quantize_load":
+        return run_quantize_load(args)
 
     import torch
     from moat_amd import _lib
@@ -315,6 +320,88 @@ def main() -> int:
                    "activations": "fp16", "output": "fp32"},
         "per_n": {str(k): v for k, v in per_n.items()},
         "roofline": roof,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+def run_quantize_load(args) -> int:
+    """Quantize-on-load of one decoder layer's weights (the 7 projections at
+    hidden 2048, fp16, 57.8 MB): the loader's rule (fp16 scale first) and the
+    144-byte records written in one kernel per tensor.  Throughput in weights/s
+    and GB/s of fp16 read + records written; the CPU baseline is the oracle
+    (quantize, then serialize) on the host."""
+    import torch
+    from moat_amd import _lib
+    from moat_amd.dequant import _float_dtype_code
+
+    lib = _lib.load()
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    rng = np.random.default_rng(LAYER_SEED)
+    host = [(rng.standard_normal((K, M), dtype=np.float32) * np.float32(0.02)).astype(np.float16) for _, K, M in LAYER]
+    layer_w = sum(K * M for _, K, M in LAYER)
+    copies = max(2, -(-ROTATE_BYTES // (2 * layer_w)))
+    ws = [[torch.from_numpy(h).to(dev) for h in host] for _ in range(copies)]
+    outs = [torch.empty((K * M // 256, 144), dtype=torch.uint8, device=dev) for _, K, M in LAYER]
+    log(f"[bench] quantize_load: 7 tensors, {layer_w / 1e6:.1f} M weights per layer, {copies} copies")
+    cap = torch.cuda.Stream()
+
+    def one_layer(c):
+        for t, o in zip(ws[c], outs):
+            w, code = _float_dtype_code(t)
+            _lib.check(lib.moat_int4_quantize_pack(w.data_ptr(), code, w.numel(), _lib.SCALE_F16, o.data_ptr(),
+                                                   cap.cuda_stream), "quantize_load")
+
+    with torch.cuda.stream(cap):
+        one_layer(0)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=cap):
+        for c in range(copies):
+            one_layer(c)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(cap):
+        graph.replay()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(cap)
+        reps = max(1, args.steps // copies)
+        for _ in range(reps):
+            graph.replay()
+        e1.record(cap)
+    e1.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / (reps * copies)
+    bytes_layer = layer_w * 2 + layer_w * 144 // 256
+    value = layer_w / (us / 1e6)
+    log(f"[bench] quantize_load: {us:.2f} us/layer, {value / 1e9:.2f} G weights/s, {bytes_layer / us / 1e3:.0f} GB/s")
+    cpu = None
+    if not args.no_cpu_baseline:
+        sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+        from oracle import superblock_oracle as O
+        t0 = time.perf_counter()
+        n_done = 0
+        for h in host:
+            q, s = O.quantize_b(h.reshape(-1))
+            O.serialize_superblocks(q, s)
+            n_done += h.size
+            if time.perf_counter() - t0 > args.cpu_budget:
+                break
+        dt = time.perf_counter() - t0
+        cpu = {"value": n_done / dt, "unit": "weights/s", "cores": 1, "kind": "port",
+               "sample": f"numpy oracle: surface-B quantize + serialize of {n_done} weights of the same layer "
+                         f"(single-threaded numpy elementwise work)"}
+        log(f"[bench] CPU baseline: {cpu['value'] / 1e6:.1f} M weights/s")
+    out = {
+        "metric": "INT4 quantize-on-load weights/s (fp16 weights to 144-byte records)",
+        "value": round(value, 1), "unit": "weights/s", "n_gpus": 1, "steps": reps * copies, "warmup": 1,
+        "ms_per_step": round(us / 1e3, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f16", "data": "synthetic",
+        "config": {"workload": "quantize-on-load of one decoder layer at hidden 2048 (7 fp16 tensors, "
+                               f"{layer_w} weights), fp16-scale rule, records written", "copies": copies},
+        "roofline": {"bound": "hbm", "achieved": round(bytes_layer / us / 1e3, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(bytes_layer / us / 1e3 / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": f"quantize_pack_kernel: {bytes_layer} B per layer (fp16 in, records out) / {us:.2f} us"},
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

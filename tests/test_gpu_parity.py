@@ -87,6 +87,7 @@ SHAPES = {
     "layer qkvo 2048x2048": (2048, 2048, 0.02, 1004, 0.0),
     "layer gate/up 2048x5632": (2048, 5632, 0.02, 1014, 0.0),
     "layer down 5632x2048": (5632, 2048, 0.02, 1024, 0.0),
+    "lm head 2048x32000": (2048, 32000, 0.02, 1006, 0.0),
 }
 
 _cache = {}
@@ -124,6 +125,7 @@ GEMM_CASES = [
     ("layer qkvo 2048x2048", [16]),
     ("layer gate/up 2048x5632", [16]),
     ("layer down 5632x2048", [16]),
+    ("lm head 2048x32000", [1, 16, 32]),
 ]
 
 
