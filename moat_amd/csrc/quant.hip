@@ -120,6 +120,75 @@ __global__ void __launch_bounds__(256) quantize_pack_kernel(const void* __restri
   }
 }
 
+// The same, four lanes per group: lane p of a group loads elements 8p..8p+7
+// with 16-byte loads (a wave covers 16 groups' contiguous bytes), the group's
+// max|w| and NaN flag are combined across the four lanes, and lane p writes
+// payload dword p of the group (lane 0 the scale).  The bits are those of
+// quantize_pack_kernel.  w must be 16-byte aligned.
+__device__ __forceinline__ void load8_f32(const void* w, int dtype, int64_t e0, float (&v)[8]) {
+  if (dtype == 1) {
+    const uint4 r = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(w) + e0);
+    const uint32_t u[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = (float)__builtin_bit_cast(_Float16, (uint16_t)(u[i] & 0xFFFFu));
+      v[2 * i + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(u[i] >> 16));
+    }
+  } else if (dtype == 0) {
+    const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(w) + e0);
+    const float4 a = p[0], b = p[1];
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  } else {
+    const double2* p = reinterpret_cast<const double2*>(static_cast<const double*>(w) + e0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const double2 d = p[i];
+      v[2 * i] = (float)d.x;
+      v[2 * i + 1] = (float)d.y;
+    }
+  }
+}
+
+__global__ void __launch_bounds__(256) quantize_pack4_kernel(const void* __restrict__ w, int dtype, int64_t n_groups,
+                                                             int scale_mode, uint8_t* __restrict__ sb) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  const int64_t total = n_groups * 4;
+  // every lane of the wave runs the same number of iterations (the shuffles
+  // need all four lanes of a group); lanes past the end load group 0 and store nothing
+  const int64_t iters = (total + stride - 1) / stride;
+  int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  for (int64_t it = 0; it < iters; ++it, t += stride) {
+    const bool live = t < total;
+    const int64_t g = live ? (t >> 2) : 0;
+    const int part = (int)(t & 3);
+    float v[8];
+    load8_f32(w, dtype, g * kGroup + 8 * part, v);
+    float amax = 0.0f;
+    int nan = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float a = fabsf(v[i]);
+      nan |= (a != a);
+      amax = fmaxf(amax, a);
+    }
+    amax = fmaxf(amax, __shfl_xor(amax, 1));
+    amax = fmaxf(amax, __shfl_xor(amax, 2));
+    nan |= __shfl_xor(nan, 1);
+    nan |= __shfl_xor(nan, 2);
+    const float s = group_scale(amax, nan != 0);
+    const _Float16 s16 = (_Float16)s;
+    const float d = scale_mode ? (float)s16 : s;
+    uint32_t word = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) word |= ((uint32_t)(quantize_one(v[i], d) + 8) & 0xFu) << (4 * i);
+    if (live) {
+      *reinterpret_cast<uint32_t*>(sb + group_payload_offset((uint64_t)g) + 4 * part) = word;
+      if (part == 0) *reinterpret_cast<uint16_t*>(sb + group_scale_offset((uint64_t)g)) = __builtin_bit_cast(uint16_t, s16);
+    }
+  }
+}
+
 static unsigned qgrid(int64_t items) {
   int64_t b = (items + 255) / 256;
   if (b < 1) b = 1;
@@ -149,8 +218,13 @@ hipError_t launch_pack_superblocks(const int8_t* q, const uint16_t* scales, int6
 
 hipError_t launch_quantize_pack(const void* w, int dtype, int64_t n, int scale_mode, uint8_t* sb, hipStream_t st) {
   const int64_t n_groups = n / kGroup;
-  hipLaunchKernelGGL(quantize_pack_kernel, dim3(qgrid(n_groups)), dim3(256), 0, st, w, dtype, n_groups, scale_mode,
-                     sb);
+  if ((reinterpret_cast<uintptr_t>(w) & 15) == 0) {
+    hipLaunchKernelGGL(quantize_pack4_kernel, dim3(qgrid(n_groups * 4)), dim3(256), 0, st, w, dtype, n_groups,
+                       scale_mode, sb);
+  } else {
+    hipLaunchKernelGGL(quantize_pack_kernel, dim3(qgrid(n_groups)), dim3(256), 0, st, w, dtype, n_groups,
+                       scale_mode, sb);
+  }
   return hipGetLastError();
 }
 
