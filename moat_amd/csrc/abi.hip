@@ -123,6 +123,12 @@ void plan_records(GemmPlan& p, int32_t n, int32_t k, int64_t groups, int64_t til
     int64_t by_traffic = k / (16 * n);
     if (by_traffic < 2) by_traffic = 2;
     if (splits > by_traffic) splits = by_traffic;
+    // ... but not below about 64 workgroups (up to 8 per group): with few
+    // column tiles the loop, not the partials, is the longer part
+    int64_t floor_splits = (64 + groups - 1) / groups;
+    if (floor_splits > 8) floor_splits = 8;
+    if (floor_splits > cap_wgs) floor_splits = cap_wgs;
+    if (splits < floor_splits) splits = floor_splits;
     if (splits < 1) splits = 1;
     // prefer a count that divides the rounds: every workgroup then holds
     // one segment of one tile group (a range that crosses a group boundary
