@@ -9,7 +9,18 @@
 // every product is accumulated in fp32, so the only difference from the CPU
 // path is the summation order.
 //
-// Tiling (one wavefront = 64 lanes, lane = 16*q + j):
+// Two kernels:
+//  * int4_gemm_records_kernel (further down), the default whenever
+//    M % 128 == 0, K % 32 == 0 and X rows are 16-byte aligned: 256-column
+//    tiles of whole 144-byte records moved into LDS by DMA, matrix cores,
+//    a stream-K split over (tile group, round) items with an in-kernel or
+//    second-kernel hand-off; it also runs several matrices sharing X in one
+//    launch and the gate/up pair with its SwiGLU epilogue;
+//  * int4_gemm_kernel (this first part), every other shape (any
+//    M % 32 == 0, ragged K, unaligned X) and the dot2 (no matrix core)
+//    variant, described next.
+//
+// General kernel tiling (one wavefront = 64 lanes, lane = 16*q + j):
 //  * a workgroup owns 128 consecutive columns of W (one column tile) and a
 //    slice of its rows; lane j owns columns 8j..8j+7 of the tile, i.e. one
 //    dword of one group per row, and lane group q owns rows 8q..8q+7 of each
@@ -39,8 +50,8 @@
 //    matching X pair, then a shuffle reduction across the 4 lane groups;
 //  * the 4 waves of a workgroup are summed through two LDS slots (32 KB at
 //    N = 32); with K split over `splits` workgroups, each publishes an fp32
-//    partial and the last one to finish a column tile adds the partials in
-//    split order, so results are deterministic;
+//    partial that a second kernel (default) or the last workgroup to finish
+//    a column tile adds in split order, so results are deterministic;
 //  * workgroup ids are remapped so that each XCD (ids are dealt round-robin
 //    to the 8 XCDs) works on one contiguous range of (split, tile) pairs:
 //    neighbouring column tiles share 128-byte lines, which then meet in the
@@ -598,8 +609,10 @@ __global__ void __launch_bounds__(kThreads) int4_gemm_kernel(GemmParams P) {
 // ---------------------------------------------------------------------------
 // Record-stream kernel: M % 128 == 0, K % 32 == 0, X rows 16-byte aligned.
 //
-// A workgroup (4 waves) owns a 256-column tile and a K slice; wave w takes
-// rounds w, w+4, ... of the slice.  In every row the tile's bytes are whole
+// A workgroup (4 or 8 waves) owns a group of 1, 2 or 4 adjacent 256-column
+// tiles and a run of (tile group, round) items (stream-K); the waves of one
+// tile take every (waves per tile)-th round of the run's segment in that
+// group.  In every row the tile's bytes are whole
 // 16-byte chunks of at most two records:
 //  * a row that starts on a record boundary (every row when M % 256 == 0,
 //    the even rows when M % 256 == 128) needs the record's header and its 8
