@@ -14,6 +14,12 @@ GPU counterpart of ``antigravity-engine/src/model_loader.py``:
   still produces that list when a caller needs it.
 * :class:`SafetensorsWeightReader` is the reference's reader (``:321-343``):
   safetensors' own loader (no pickle), fp16 out.
+* :meth:`ModelWeightLoader.parse_gguf_file` / :meth:`ModelWeightLoader.auto_load_gguf`:
+  the reference's GGUF header parser and loader (``:137-251``): F32 and F16
+  tensors, and its int8 fallback for every other tensor type.
+* :func:`estimate_model_superblock_memory`, :class:`SuperBlockRepacker`,
+  :class:`QuantizedSuperBlockTensor` and :class:`MemoryBudgetValidator`: the
+  reference's helpers (``:281-403``) with the records on the GPU.
 * :func:`save_superblocks` / :func:`load_superblocks`: a record file (magic,
   original shape, then the records as written) so that quantization runs once.
 """
@@ -28,10 +34,11 @@ import numpy as np
 import torch
 
 from . import _device as D
-from .dequant import SUPERBLOCK_BYTES, SUPERBLOCK_ELEMS, quantize_to_superblocks, unpack_superblock_weights
+from .dequant import GROUP_SIZE, SUPERBLOCK_BYTES, SUPERBLOCK_ELEMS, quantize_to_superblocks, unpack_superblock_weights
 from .engine_dequant import quantize_weights_int4
 
-MODEL_WEIGHT_BUDGET_BYTES = int(2.5 * 1024 ** 3)  # model_loader.py's default budget (2.5 GB)
+IOS_APP_MEMORY_CEILING_BYTES = 4500 * 1024 * 1024  # model_loader.py:21
+MODEL_WEIGHT_BUDGET_BYTES = 2500 * 1024 * 1024  # model_loader.py:22, the loader's default budget
 RECORD_FILE_MAGIC = b"MOATI4R1"
 
 
@@ -42,6 +49,7 @@ class ModelWeightLoader:
         self.memory_budget_bytes = memory_budget_bytes
         self.layers: Dict[str, Dict] = {}
         self.total_loaded_bytes = 0
+        self._host_io = set()
 
     def load_and_repack_layer(self, layer_name: str, weights_fp16, group_size: int = 32,
                               keep_q: bool = True) -> Dict:
@@ -67,6 +75,10 @@ class ModelWeightLoader:
                 f"memory budget of {self.memory_budget_bytes / 1e9:.2f} GB. "
                 f"Currently loaded: {self.total_loaded_bytes / 1e9:.2f} GB.")
         records = quantize_to_superblocks(w, scale_rule="f16")
+        if D.is_tensor(weights_fp16) and weights_fp16.is_cuda:
+            self._host_io.discard(layer_name)
+        else:
+            self._host_io.add(layer_name)  # numpy in: dequantize_layer hands numpy back
         layer = {
             "layer_name": layer_name,
             "original_shape": original_shape,
@@ -85,12 +97,70 @@ class ModelWeightLoader:
     def dequantize_layer(self, layer_name: str) -> torch.Tensor:
         """fp16 weights of a loaded layer in its original shape, decoded on the
         GPU from the records (``model_loader.py:110-134``; same bits as its
-        LUT route)."""
+        LUT route): numpy when the layer was loaded from host data, else a
+        GPU tensor."""
         if layer_name not in self.layers:
             raise KeyError(f"Layer '{layer_name}' not found in loader")
         layer = self.layers[layer_name]
         flat = unpack_superblock_weights(layer["superblocks"], layer["superblocks"].shape[0])
-        return flat[: layer["n_elements"]].reshape(layer["original_shape"])
+        out = flat[: layer["n_elements"]].reshape(layer["original_shape"])
+        return D.to_host(out) if layer_name in self._host_io else out
+
+    def unload_layer(self, layer_name: str) -> None:
+        """Drop a layer (its records are freed with the last reference) and
+        return its bytes to the budget (``model_loader.py:264-269``)."""
+        if layer_name in self.layers:
+            self.total_loaded_bytes -= self.layers.pop(layer_name)["memory_bytes"]
+            self._host_io.discard(layer_name)
+
+    def clear(self) -> None:
+        """Drop every layer (``model_loader.py:271-274``)."""
+        self.layers.clear()
+        self._host_io.clear()
+        self.total_loaded_bytes = 0
+
+    def parse_gguf_file(self, gguf_path: str) -> Dict:
+        """GGUF header: metadata key/values, tensor table (name, dims as
+        stored, type, offset) and the aligned start of the tensor data
+        (``model_loader.py:137-214``).  Raises FileNotFoundError for a missing
+        file and ValueError for a bad magic or an unknown value type."""
+        if not os.path.exists(gguf_path):
+            raise FileNotFoundError(f"GGUF weight file not found at: {gguf_path}")
+        with open(gguf_path, "rb") as f:
+            return _GGUFHeader(f).parse()
+
+    def auto_load_gguf(self, gguf_path: str) -> Dict:
+        """Load every tensor of a GGUF file as INT4 records
+        (``model_loader.py:217-251``): F32 (type 0) is rounded to fp16 on the
+        GPU, F16 (type 1) is taken as stored, and any other type is read as
+        one int8 per element (zero-filled past the end of the file) and
+        mapped to fp16(int8 / 7), as the reference does.  The shape is the
+        dims in stored order.  Returns the parsed header."""
+        if not os.path.exists(gguf_path):
+            raise FileNotFoundError(f"GGUF model file not found at '{gguf_path}'. Please provide a valid file path.")
+        info = self.parse_gguf_file(gguf_path)
+        base = info.get("tensor_data_offset", 0)
+        dev = D.require_gpu()
+        with open(gguf_path, "rb") as f:
+            for name, t in info["tensors"].items():
+                shape = tuple(int(d) for d in t["dims"])
+                n = int(np.prod(shape, dtype=np.int64)) if shape else 1
+                f.seek(base + t["offset"])
+                if t["type"] == 0:
+                    host = np.frombuffer(f.read(4 * n), dtype=np.float32)
+                    w = torch.from_numpy(host.copy()).to(dev).to(torch.float16)
+                elif t["type"] == 1:
+                    w = torch.from_numpy(np.frombuffer(f.read(2 * n), dtype=np.float16).copy()).to(dev)
+                else:
+                    raw = f.read(n)
+                    raw = raw + b"\x00" * (n - len(raw))
+                    q = torch.from_numpy(np.frombuffer(raw, dtype=np.int8).copy()).to(dev)
+                    # int8 -> fp16 is exact; the quotient by 7 in fp32 (correctly
+                    # rounded elementwise division), then one rounding to fp16
+                    seven = torch.full_like(q, 7, dtype=torch.float32)
+                    w = (q.to(torch.float32) / seven).to(torch.float16)
+                self.load_and_repack_layer(name, w.reshape(shape))
+        return info
 
     def load_safetensors(self, path: str, names: Optional[Iterable[str]] = None) -> Dict[str, Dict]:
         """Quantize-on-load of a safetensors checkpoint: every tensor (or those
@@ -109,6 +179,144 @@ class ModelWeightLoader:
     @property
     def total_memory_gb(self) -> float:
         return self.total_loaded_bytes / (1024 ** 3)
+
+
+class _GGUFHeader:
+    """Reader of a GGUF header (little-endian): magic, version, tensor count,
+    key/value count, the key/values, the tensor table."""
+
+    # value type -> struct code of the scalar types (GGUF value-type table)
+    _SCALAR = {0: "<B", 1: "<b", 2: "<H", 3: "<h", 4: "<I", 5: "<i", 6: "<f", 7: "<?", 10: "<Q", 11: "<q", 12: "<d"}
+    _STRING, _ARRAY = 8, 9
+
+    def __init__(self, f):
+        self.f = f
+
+    def _unpack(self, code: str):
+        size = struct.calcsize(code)
+        data = self.f.read(size)
+        if len(data) != size:
+            raise ValueError("GGUF header is truncated")
+        return struct.unpack(code, data)[0]
+
+    def _string(self) -> str:
+        return self.f.read(self._unpack("<Q")).decode("utf-8", errors="replace")
+
+    def _value(self, vtype: int):
+        if vtype in self._SCALAR:
+            return self._unpack(self._SCALAR[vtype])
+        if vtype == self._STRING:
+            return self._string()
+        if vtype == self._ARRAY:
+            etype = self._unpack("<I")
+            count = self._unpack("<Q")
+            return [self._value(etype) for _ in range(count)]
+        raise ValueError(f"Unknown value type: {vtype}")
+
+    def parse(self) -> Dict:
+        magic = self.f.read(4)
+        if magic != b"GGUF":
+            raise ValueError(f"Invalid GGUF magic header: {magic}")
+        version = self._unpack("<I")
+        n_tensors = self._unpack("<Q")
+        n_kv = self._unpack("<Q")
+        metadata = {}
+        for _ in range(n_kv):
+            key = self._string()
+            metadata[key] = self._value(self._unpack("<I"))
+        tensors = {}
+        for _ in range(n_tensors):
+            name = self._string()
+            dims = [self._unpack("<Q") for _ in range(self._unpack("<I"))]
+            ttype = self._unpack("<I")
+            tensors[name] = {"name": name, "dims": dims, "type": ttype, "offset": self._unpack("<Q")}
+        end = self.f.tell()
+        align = int(metadata.get("general.alignment", 32))
+        return {"metadata": metadata, "tensors": tensors, "version": version, "n_tensors": n_tensors,
+                "tensor_data_offset": end + (-end) % align}
+
+
+def estimate_model_superblock_memory(n_parameters: int, group_size: int = 32) -> Dict[str, float]:
+    """Footprint of a model stored as 144-byte records (``model_loader.py:281-318``):
+    ceil(P / 256) records against 2 bytes per fp16 weight."""
+    records_bytes = -(-int(n_parameters) // SUPERBLOCK_ELEMS) * SUPERBLOCK_BYTES
+    fp16_bytes = int(n_parameters) * 2
+    mib = 1024.0 * 1024.0
+    return {
+        "n_parameters": n_parameters,
+        "fp16_memory_mb": fp16_bytes / mib,
+        "superblock_memory_mb": records_bytes / mib,
+        "superblock_memory_gb": records_bytes / mib / 1024.0,
+        "compression_ratio": fp16_bytes / records_bytes,
+        "bits_per_weight": SUPERBLOCK_BYTES * 8 / SUPERBLOCK_ELEMS,
+        "fits_ios_4_5gb_ceiling": records_bytes <= MODEL_WEIGHT_BUDGET_BYTES,
+    }
+
+
+class QuantizedSuperBlockTensor:
+    """A weight tensor held as 144-byte records on the GPU with its original
+    shape (``model_loader.py:344-360``)."""
+
+    def __init__(self, superblocks, shape, group_size: int = 32, host_io: bool = False):
+        self.superblocks = superblocks
+        self.shape = tuple(shape)
+        self.group_size = group_size
+        self.bytes_per_superblock = SUPERBLOCK_BYTES
+        self.memory_bytes = len(superblocks) * SUPERBLOCK_BYTES
+        self._host_io = host_io
+
+    def validate_structure(self) -> bool:
+        """Every record is 144 bytes: 8 fp16 scales (16 bytes) then 128
+        payload bytes, and the records cover the shape."""
+        sb = self.superblocks
+        ok = sb.dim() == 2 and sb.shape[1] == SUPERBLOCK_BYTES and sb.dtype == torch.uint8
+        return bool(ok and sb.shape[0] * SUPERBLOCK_ELEMS >= int(np.prod(self.shape, dtype=np.int64)))
+
+    def dequantize(self):
+        """fp16 weights in the original shape (numpy when packed from host data)."""
+        flat = unpack_superblock_weights(self.superblocks, self.superblocks.shape[0])
+        out = flat[: int(np.prod(self.shape, dtype=np.int64))].reshape(self.shape)
+        return D.to_host(out) if self._host_io else out
+
+
+class SuperBlockRepacker:
+    """``model_loader.py:363-375``: fp16 cast, zero pad to 256, fp16-scale
+    quantizer, records -- one GPU kernel after the cast."""
+
+    @staticmethod
+    def repack_matrix(matrix, group_size: int = 32, groups_per_superblock: int = 8) -> QuantizedSuperBlockTensor:
+        if group_size != GROUP_SIZE or groups_per_superblock != SUPERBLOCK_ELEMS // GROUP_SIZE:
+            raise ValueError("the 144-byte records hold 8 groups of 32 weights")
+        shape = tuple(matrix.shape)
+        w = D.to_device(matrix).reshape(-1).to(torch.float16)
+        rem = w.numel() % SUPERBLOCK_ELEMS
+        if rem:
+            w = torch.cat([w, torch.zeros(SUPERBLOCK_ELEMS - rem, dtype=torch.float16, device=w.device)])
+        records = quantize_to_superblocks(w, scale_rule="f16")
+        host_io = not (D.is_tensor(matrix) and matrix.is_cuda)
+        return QuantizedSuperBlockTensor(records, shape, group_size=group_size, host_io=host_io)
+
+
+class MemoryBudgetValidator:
+    """``model_loader.py:378-403``: weights as records plus an fp16 KV cache
+    (16 heads x 64 dims, keys and values) against 2.5 GB / 4.5 GB."""
+
+    @staticmethod
+    def calculate_weight_memory_gb(num_params: int) -> float:
+        return (-(-int(num_params) // SUPERBLOCK_ELEMS) * SUPERBLOCK_BYTES) / 1024.0 ** 3
+
+    @staticmethod
+    def validate_memory_budget(num_params: int, num_traces: int = 8, seq_len: int = 2048,
+                               runtime_overhead_gb: float = 0.5) -> Dict:
+        weight_gb = MemoryBudgetValidator.calculate_weight_memory_gb(num_params)
+        kv_gb = num_traces * seq_len * 16 * 64 * 2 * 2 / 1024.0 ** 3
+        total_gb = weight_gb + kv_gb + runtime_overhead_gb
+        weight_ok = weight_gb <= 2.5
+        app_ok = total_gb <= 4.5
+        if not (weight_ok and app_ok):
+            raise ValueError(f"Memory budget breached: weight={weight_gb:.2f}GB, total={total_gb:.2f}GB")
+        return {"weight_memory_gb": weight_gb, "total_app_memory_gb": total_gb,
+                "weight_budget_passed": weight_ok, "total_app_budget_passed": app_ok, "is_valid": True}
 
 
 class SafetensorsWeightReader:
@@ -138,6 +346,9 @@ class SafetensorsWeightReader:
         if name not in self.f:
             raise KeyError(f"Tensor '{name}' not found in Safetensors file {self.model_path}.")
         return D.to_device(self.f[name])
+
+
+GGUFWeightReader = SafetensorsWeightReader  # model_loader.py:341, the same reader under the GGUF name
 
 
 def save_superblocks(path: str, records, original_shape: Tuple[int, ...]) -> None:

@@ -73,7 +73,8 @@ def test_gpu_loader_matches_oracle(shape):
     assert layer["memory_bytes"] == records.shape[0] * 144
     assert np.array_equal(layer["superblocks"].cpu().numpy(), records)
     assert np.array_equal(layer["q_weights"], q) and np.array_equal(layer["scales"].view(np.uint16), s.view(np.uint16))
-    deq = loader.dequantize_layer("x").cpu().numpy()
+    deq = loader.dequantize_layer("x")  # numpy in, numpy out
+    assert isinstance(deq, np.ndarray)
     want = O.decode_superblocks(records, records.shape[0])[: int(np.prod(shape))].reshape(shape)
     assert deq.shape == shape and np.array_equal(deq.view(np.uint16), want.view(np.uint16))
     assert loader.total_loaded_bytes == records.shape[0] * 144
@@ -101,3 +102,187 @@ def test_gpu_loader_budget_and_safetensors(tmp_path):
         save_superblocks(rec_path, layers[name]["superblocks"], layers[name]["original_shape"])
         back, shape = load_superblocks(rec_path, device=True)
         assert shape == tuple(t.shape) and torch.equal(back, layers[name]["superblocks"])
+
+
+# ---------------------------------------------------------------------------
+# GGUF files (written here with the GGUF layout: little-endian header, typed
+# key/values, tensor table, data aligned to general.alignment)
+
+def _gguf_bytes(kvs, tensors, alignment=None):
+    """kvs: [(key, vtype, value)] (vtype 9 = (elem_type, [values])); tensors:
+    [(name, dims, ttype, payload bytes)].  Returns the file bytes and the
+    expected data offset."""
+    import struct
+
+    def s(text):
+        b = text.encode()
+        return struct.pack("<Q", len(b)) + b
+
+    scalar = {0: "<B", 1: "<b", 2: "<H", 3: "<h", 4: "<I", 5: "<i", 6: "<f", 7: "<?", 10: "<Q", 11: "<q", 12: "<d"}
+
+    def val(vt, v):
+        if vt in scalar:
+            return struct.pack(scalar[vt], v)
+        if vt == 8:
+            return s(v)
+        et, items = v
+        return struct.pack("<I", et) + struct.pack("<Q", len(items)) + b"".join(val(et, i) for i in items)
+
+    kvs = list(kvs)
+    if alignment is not None:
+        kvs.append(("general.alignment", 4, alignment))
+    align = alignment or 32
+    head = b"GGUF" + struct.pack("<I", 3) + struct.pack("<Q", len(tensors)) + struct.pack("<Q", len(kvs))
+    for k, vt, v in kvs:
+        head += s(k) + struct.pack("<I", vt) + val(vt, v)
+    offsets, off = [], 0
+    for _, _, _, payload in tensors:
+        offsets.append(off)
+        off += len(payload) + (-len(payload)) % align
+    for (name, dims, tt, _), o in zip(tensors, offsets):
+        head += s(name) + struct.pack("<I", len(dims)) + b"".join(struct.pack("<Q", d) for d in dims)
+        head += struct.pack("<I", tt) + struct.pack("<Q", o)
+    data_off = len(head) + (-len(head)) % align
+    body = bytearray(head + b"\0" * (data_off - len(head)))
+    for (_, _, _, payload), o in zip(tensors, offsets):
+        body += b"\0" * (data_off + o - len(body)) + payload
+    return bytes(body), data_off
+
+
+def test_gguf_header_parse(tmp_path):
+    from moat_amd.loader import ModelWeightLoader
+    kvs = [("general.name", 8, "tiny"), ("u8", 0, 250), ("i8", 1, -5), ("u16", 2, 65000), ("i16", 3, -300),
+           ("u32", 4, 4000000000), ("i32", 5, -7), ("f32", 6, 0.5), ("flag", 7, True), ("u64", 10, 2 ** 40),
+           ("i64", 11, -2 ** 40), ("f64", 12, 0.125), ("arr", 9, (5, [1, -2, 3])), ("names", 9, (8, ["a", "bc"]))]
+    w = np.arange(12, dtype=np.float32)
+    blob, data_off = _gguf_bytes(kvs, [("w", [3, 4], 0, w.tobytes()), ("h", [8], 1, np.ones(8, np.float16).tobytes())],
+                                 alignment=64)
+    path = os.path.join(tmp_path, "m.gguf")
+    open(path, "wb").write(blob)
+    info = ModelWeightLoader().parse_gguf_file(path)
+    md = info["metadata"]
+    assert info["version"] == 3 and info["n_tensors"] == 2
+    assert md["general.name"] == "tiny" and md["u8"] == 250 and md["i8"] == -5 and md["u16"] == 65000
+    assert md["i16"] == -300 and md["u32"] == 4000000000 and md["i32"] == -7 and md["f32"] == 0.5
+    assert md["flag"] is True and md["u64"] == 2 ** 40 and md["i64"] == -2 ** 40 and md["f64"] == 0.125
+    assert md["arr"] == [1, -2, 3] and md["names"] == ["a", "bc"] and md["general.alignment"] == 64
+    assert info["tensors"]["w"] == {"name": "w", "dims": [3, 4], "type": 0, "offset": 0}
+    assert info["tensors"]["h"]["offset"] == 64 and info["tensors"]["h"]["type"] == 1
+    assert info["tensor_data_offset"] == data_off and data_off % 64 == 0
+    # default alignment 32
+    blob32, off32 = _gguf_bytes([("k", 8, "v")], [("w", [4], 0, w[:4].tobytes())])
+    open(path, "wb").write(blob32)
+    assert ModelWeightLoader().parse_gguf_file(path)["tensor_data_offset"] == off32 and off32 % 32 == 0
+
+
+def test_gguf_header_errors(tmp_path):
+    from moat_amd.loader import ModelWeightLoader
+    loader = ModelWeightLoader()
+    path = os.path.join(tmp_path, "bad.gguf")
+    with pytest.raises(FileNotFoundError):
+        loader.parse_gguf_file(path)
+    with pytest.raises(FileNotFoundError):
+        loader.auto_load_gguf(path)
+    open(path, "wb").write(b"GGML" + bytes(20))
+    with pytest.raises(ValueError, match="magic"):
+        loader.parse_gguf_file(path)
+    blob, _ = _gguf_bytes([("k", 8, "v")], [])
+    open(path, "wb").write(blob.replace(b"\x08\x00\x00\x00", b"\x0d\x00\x00\x00", 1))  # value type 13
+    with pytest.raises(ValueError, match="Unknown value type: 13"):
+        loader.parse_gguf_file(path)
+
+
+def test_memory_estimates():
+    """model_loader.py:281-318 and :378-403, with the reference tests' cases
+    (test_batch_generator.py:192-199, test_model_loader.py:106-149) and the
+    closed forms."""
+    from moat_amd.loader import MODEL_WEIGHT_BUDGET_BYTES, MemoryBudgetValidator, estimate_model_superblock_memory
+    est = estimate_model_superblock_memory(1_500_000_000)
+    assert est["superblock_memory_mb"] * 2 ** 20 == 5_859_375 * 144          # 1.5e9 / 256 records exactly
+    assert est["superblock_memory_gb"] <= 2.5 and est["fits_ios_4_5gb_ceiling"] and est["bits_per_weight"] == 4.5
+    assert est["compression_ratio"] == 3e9 / (5_859_375 * 144) and est["fp16_memory_mb"] == 3e9 / 2 ** 20
+    assert estimate_model_superblock_memory(257)["superblock_memory_mb"] * 2 ** 20 == 2 * 144  # ceil
+    big = MODEL_WEIGHT_BUDGET_BYTES // 144 * 256 + 256
+    assert not estimate_model_superblock_memory(big)["fits_ios_4_5gb_ceiling"]
+    assert MODEL_WEIGHT_BUDGET_BYTES == 2500 * 2 ** 20
+    gb = MemoryBudgetValidator.calculate_weight_memory_gb(1_540_000_000)
+    assert gb == 6_015_625 * 144 / 2 ** 30 and 0.7 < gb <= 2.5
+    rep = MemoryBudgetValidator.validate_memory_budget(1_540_000_000, num_traces=8, seq_len=2048,
+                                                       runtime_overhead_gb=0.5)
+    assert rep["total_app_memory_gb"] == gb + 8 * 2048 * 16 * 64 * 4 / 2 ** 30 + 0.5
+    assert rep["weight_budget_passed"] and rep["total_app_budget_passed"] and rep["is_valid"]
+    with pytest.raises(ValueError):
+        MemoryBudgetValidator.validate_memory_budget(num_params=6_000_000_000)
+    with pytest.raises(ValueError):  # weights fit, the KV cache does not
+        MemoryBudgetValidator.validate_memory_budget(1_000_000_000, num_traces=512)
+
+
+@pytest.mark.gpu
+def test_gpu_auto_load_gguf(tmp_path):
+    """F32 rounded to fp16, F16 as stored, and the int8 fallback over all 256
+    byte values (fp16 of int8 / 7, computed here as numpy computes it), each
+    packed bit-exactly like the oracle; a short tensor is zero-filled."""
+    from moat_amd.loader import ModelWeightLoader
+    print("case: auto_load_gguf", flush=True)
+    rng = np.random.default_rng(12)
+    f32 = (rng.standard_normal((16, 48)) * 0.05).astype(np.float32)
+    f32[0, :4] = [1000.0, -1e-8, 0.0, 65504.0]  # fp16 max, and a value that rounds to -0
+    f16 = (rng.standard_normal(320) * 0.1).astype(np.float16)
+    i8 = np.arange(-128, 128, dtype=np.int8)
+    short = np.tile(i8, 2)[:300]
+    tensors = [("a", [16, 48], 0, f32.tobytes()), ("b", [320], 1, f16.tobytes()), ("c", [256], 24, i8.tobytes()),
+               ("d", [2, 256], 30, short.tobytes())]  # last tensor: 300 of 512 bytes in the file
+    blob, _ = _gguf_bytes([("general.name", 8, "t")], tensors)
+    path = os.path.join(tmp_path, "m.gguf")
+    open(path, "wb").write(blob)
+    loader = ModelWeightLoader()
+    hdr = loader.parse_gguf_file(path)
+    open(path, "wb").write(blob[: hdr["tensor_data_offset"] + hdr["tensors"]["d"]["offset"] + 300])
+    info = loader.auto_load_gguf(path)
+    assert sorted(info["tensors"]) == ["a", "b", "c", "d"]
+    d = np.concatenate([short, np.zeros(212, np.int8)])
+    want = {"a": f32.astype(np.float16), "b": f16, "c": i8.astype(np.float16) / 7.0,
+            "d": (d.astype(np.float16) / 7.0).reshape(2, 256)}
+    for name, w in want.items():
+        assert w.dtype == np.float16
+        _, _, records, _ = _oracle_layer(w)
+        layer = loader.layers[name]
+        assert layer["original_shape"] == w.shape, name
+        assert np.array_equal(layer["superblocks"].cpu().numpy(), records), name
+
+
+@pytest.mark.gpu
+def test_gpu_repacker_and_layer_bookkeeping():
+    """SuperBlockRepacker / QuantizedSuperBlockTensor (test_model_loader.py:70-99
+    cases, plus the oracle's bits), host-in/host-out dequantize_layer, and
+    unload_layer / clear returning bytes to the budget."""
+    from moat_amd.loader import ModelWeightLoader, SuperBlockRepacker
+    print("case: repacker + bookkeeping", flush=True)
+    matrix = np.random.default_rng(42).standard_normal((256, 256)).astype(np.float16)
+    qt = SuperBlockRepacker.repack_matrix(matrix, group_size=32, groups_per_superblock=8)
+    assert qt.validate_structure() and qt.bytes_per_superblock == 144
+    assert len(qt.superblocks) == 256 and qt.memory_bytes == 256 * 144
+    _, _, records, _ = _oracle_layer(matrix)
+    assert np.array_equal(qt.superblocks.cpu().numpy(), records)
+    original = np.random.default_rng(99).standard_normal((128, 256)).astype(np.float16)
+    deq = SuperBlockRepacker.repack_matrix(original).dequantize()
+    assert isinstance(deq, np.ndarray) and deq.shape == original.shape and deq.dtype == np.float16
+    _, _, rec2, _ = _oracle_layer(original)
+    assert np.array_equal(deq.reshape(-1).view(np.uint16), O.decode_superblocks(rec2, rec2.shape[0]).view(np.uint16))
+    assert float(np.mean(np.abs(original.astype(np.float32) - deq.astype(np.float32)))) < 0.2
+    with pytest.raises(ValueError):
+        SuperBlockRepacker.repack_matrix(original, group_size=64)
+
+    loader = ModelWeightLoader()
+    w = np.random.default_rng(5).standard_normal((256, 256)).astype(np.float16)
+    loader.load_and_repack_layer("layer_0", w)
+    out = loader.dequantize_layer("layer_0")
+    assert isinstance(out, np.ndarray) and out.shape == (256, 256) and out.dtype == np.float16
+    loader.load_and_repack_layer("layer_1", torch.from_numpy(w).cuda())
+    assert loader.dequantize_layer("layer_1").is_cuda
+    assert loader.total_loaded_bytes == 2 * 256 * 144
+    loader.unload_layer("layer_0")
+    loader.unload_layer("missing")
+    assert loader.total_loaded_bytes == 256 * 144 and list(loader.layers) == ["layer_1"]
+    loader.clear()
+    assert loader.total_loaded_bytes == 0 and not loader.layers
