@@ -247,6 +247,48 @@ int32_t moat_int4_any_negative(const int64_t* q, int64_t n, int32_t* flag_out, h
 int32_t moat_int4_to_f16(const void* src, int32_t src_dtype, int64_t n, uint16_t* out_f16,
                          hipStream_t stream);
 
+/*
+ * Token sampling from LM-head logits (the numpy path of
+ * BatchedRolloutCoordinator.sample_tokens, antigravity-engine/src/batch_generator.py:187-253,
+ * and the table softmax it calls, antigravity-engine/src/attention.py:97-135).
+ *
+ * `lut_f16` is the exp table of ExponentialLUT (attention.py:32-58): lut_size
+ * fp16 values of exp over [-range_max, 0], 2 <= lut_size <= 32768; `step` is
+ * range_max / (lut_size - 1) rounded to float32.  Logits are [n][v] of dtype
+ * F32, F16 or F64, 1 <= v <= 32768, one row per workgroup.
+ *
+ * moat_lut_softmax: probs_f16[n][v] = safe_softmax_lut(x) along each row:
+ * row max (f32), table index size-1-trunc(min(|x - max| / step, size-1)),
+ * numpy's float32 pairwise sum of the table values, fp16(e / sum).  A row
+ * whose maximum is NaN or infinite (the reference's index is undefined
+ * there) gives NaN.
+ */
+int32_t moat_lut_softmax(const void* x, int32_t dtype, int32_t n, int32_t v, const uint16_t* lut_f16,
+                         int32_t lut_size, float step, uint16_t* probs_f16, hipStream_t stream);
+
+/*
+ * moat_sample_tokens: temperature <= 0: greedy, tokens[r] = np.argmax(row r)
+ * (first maximum, NaN first), logprobs[r] = fp16(log(p[token])) (an fp16
+ * value in a float), p the table softmax of the raw logits.  temperature > 0:
+ * p = table softmax of logits / max(temperature, 1e-5) (divided in the
+ * logits' dtype); the top_k (1..64; min(top_k, v)) largest p, ordered by p
+ * descending then index ascending (the reference leaves the order to
+ * np.argpartition), renormalised in float32 (numpy's summation order), one
+ * draw u of row r from a counter-based generator (SplitMix64 of seed +
+ * (r + 1) * 0x9E3779B97F4A7C15, 53 bits), the first entry of the float64
+ * cumulative distribution above u; logprobs[r] = float32 log of the token's
+ * full-softmax p (log(1e-10) when p is 0).  tokens int32, logprobs float32.
+ * A row whose maximum is NaN or infinite: the argmax token and a NaN log.
+ */
+int32_t moat_sample_tokens(const void* logits, int32_t dtype, int32_t n, int32_t v, double temperature,
+                           int32_t top_k, uint64_t seed, const uint16_t* lut_f16, int32_t lut_size,
+                           float step, int32_t* tokens, float* logprobs, hipStream_t stream);
+
+/* ExponentialLUT.lookup (attention.py:60-85): out_f16[i] =
+ * lut[size-1-trunc(min(|x[i]| / step, size-1))] for float32 x (NaN -> NaN). */
+int32_t moat_lut_lookup(const float* x, int64_t n, const uint16_t* lut_f16, int32_t lut_size, float step,
+                        uint16_t* out_f16, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -33,6 +33,11 @@ int gemm_fused_groups(int mode, int mats, int m);
 hipError_t launch_gemm_fused(int mode, const uint16_t* x, const uint8_t* const* sbs, float* const* ys, uint16_t* h,
                              int mats, int n, int k, int m, int wgs, int depth, int finish, float* partials,
                              hipStream_t stream);
+hipError_t launch_lut_sample(const void* x, int dtype, int n, int v, double temp, int scaled, const uint16_t* lut,
+                             int lut_size, float step, int mode, int top_k, uint64_t seed, int32_t* tokens,
+                             float* logprobs, uint16_t* probs, hipStream_t st);
+hipError_t launch_lut_lookup(const float* x, int64_t n, const uint16_t* lut, int lut_size, float step, uint16_t* out,
+                             hipStream_t st);
 hipError_t launch_gemm(int algo, const uint16_t* x, const uint8_t* sb, float* y, int n, int k, int m, int splits,
                        int batch, int finish, int front, int group, int waves, float* partials,
                        uint32_t* counters, hipStream_t stream);
@@ -257,6 +262,20 @@ int32_t run_fused(int mode, const uint16_t* x, const uint8_t* const* sbs, float*
                                            partials, stream));
 }
 
+// Shared checks of the sampling entry points: dtype, 1 <= v <= 32768 (a row
+// in one workgroup), table of 2..32768 fp16 entries, positive finite step.
+bool sample_args_ok(const void* x, int32_t dtype, int32_t n, int32_t v, const uint16_t* lut, int32_t lut_size,
+                    float step) {
+  if (dtype != MOAT_DTYPE_F32 && dtype != MOAT_DTYPE_F16 && dtype != MOAT_DTYPE_F64) return false;
+  if (n < 0 || v < 1 || v > 32768 || lut_size < 2 || lut_size > 32768) return false;
+  if (!(step > 0.f) || step == INFINITY) return false;
+  if (n == 0) return true;
+  const uintptr_t elem = dtype == MOAT_DTYPE_F32 ? 4 : dtype == MOAT_DTYPE_F16 ? 2 : 8;
+  return x && lut && aligned(x, elem) && aligned(lut, 2);
+}
+
+int sample_dtype(int32_t dtype) { return dtype == MOAT_DTYPE_F32 ? 0 : dtype == MOAT_DTYPE_F16 ? 1 : 2; }
+
 }  // namespace
 
 extern "C" {
@@ -438,6 +457,41 @@ int32_t moat_int4_to_f16(const void* src, int32_t src_dtype, int64_t n, uint16_t
   if (!src || !out_f16) return MOAT_ERR_INVALID;
   if (!aligned(src, src_dtype == MOAT_DTYPE_F64 ? 8 : 4) || !aligned(out_f16, 2)) return MOAT_ERR_INVALID;
   return status_of(moat::launch_to_f16(src, src_dtype, n, out_f16, stream));
+}
+
+// ---- token sampling ----
+
+int32_t moat_lut_softmax(const void* x, int32_t dtype, int32_t n, int32_t v, const uint16_t* lut_f16,
+                         int32_t lut_size, float step, uint16_t* probs_f16, hipStream_t stream) {
+  if (!sample_args_ok(x, dtype, n, v, lut_f16, lut_size, step)) return MOAT_ERR_INVALID;
+  if (n > 0 && (!probs_f16 || !aligned(probs_f16, 2))) return MOAT_ERR_INVALID;
+  return status_of(moat::launch_lut_sample(x, sample_dtype(dtype), n, v, 1.0, 0, lut_f16, lut_size, step, 0, 1, 0,
+                                           nullptr, nullptr, probs_f16, stream));
+}
+
+int32_t moat_sample_tokens(const void* logits, int32_t dtype, int32_t n, int32_t v, double temperature,
+                           int32_t top_k, uint64_t seed, const uint16_t* lut_f16, int32_t lut_size, float step,
+                           int32_t* tokens, float* logprobs, hipStream_t stream) {
+  if (!sample_args_ok(logits, dtype, n, v, lut_f16, lut_size, step)) return MOAT_ERR_INVALID;
+  if (!(temperature == temperature) || top_k < 1 || top_k > 64) return MOAT_ERR_INVALID;
+  if (n > 0 && (!tokens || !logprobs || !aligned(tokens, 4) || !aligned(logprobs, 4))) return MOAT_ERR_INVALID;
+  const bool greedy = temperature <= 0.0;
+  // logits / max(T, 1e-5) with T rounded to the logits' dtype first (numpy's
+  // array / Python float)
+  double t = temperature > 1e-5 ? temperature : 1e-5;
+  if (dtype == MOAT_DTYPE_F32) t = (double)(float)t;
+  if (dtype == MOAT_DTYPE_F16) t = (double)(_Float16)t;
+  return status_of(moat::launch_lut_sample(logits, sample_dtype(dtype), n, v, t, greedy ? 0 : 1, lut_f16, lut_size,
+                                           step, greedy ? 1 : 2, top_k, seed, tokens, logprobs, nullptr, stream));
+}
+
+int32_t moat_lut_lookup(const float* x, int64_t n, const uint16_t* lut_f16, int32_t lut_size, float step,
+                        uint16_t* out_f16, hipStream_t stream) {
+  if (n < 0 || lut_size < 2 || !(step > 0.f) || step == INFINITY) return MOAT_ERR_INVALID;
+  if (n == 0) return MOAT_OK;
+  if (!x || !lut_f16 || !out_f16 || !aligned(x, 4) || !aligned(lut_f16, 2) || !aligned(out_f16, 2))
+    return MOAT_ERR_INVALID;
+  return status_of(moat::launch_lut_lookup(x, n, lut_f16, lut_size, step, out_f16, stream));
 }
 
 }  // extern "C"

@@ -15,7 +15,7 @@ HEADER = os.path.join(ROOT, "include", "moat_int4.h")
 
 def _declared_symbols():
     text = open(HEADER).read()
-    return sorted(set(re.findall(r"\b(moat_int4_\w+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b(moat_\w+)\s*\(", text)))
 
 
 @pytest.fixture(scope="module")
@@ -37,7 +37,7 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
 def _declared_arities():
     text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
     out = {}
-    for name, args in re.findall(r"\b(moat_int4_\w+)\s*\(([^)]*)\)\s*;", text):
+    for name, args in re.findall(r"\b(moat_\w+)\s*\(([^)]*)\)\s*;", text):
         args = args.strip()
         out[name] = 0 if args in ("", "void") else args.count(",") + 1
     return out
@@ -174,6 +174,52 @@ def test_fused_entry_points_validate(lib):
         P3 = ctypes.c_void_p * 3
         assert lib.moat_int4_gemm_multi(FAKE, P3(*[FAKE.value] * 3), P3(*[FAKE.value] * 3), 3, 1, 2048, 2048,
                                         FAKE, size - 1, None) == _lib.MOAT_ERR_WORKSPACE
+
+
+def test_sampling_entry_points_validate(lib):
+    I = _lib.MOAT_ERR_INVALID
+    F = ctypes.c_float
+    step = F(10.0 / 32767)
+    ok = dict(dtype=0, n=2, v=1000, lut_size=32768)
+    # moat_lut_softmax(x, dtype, n, v, lut, lut_size, step, probs, stream)
+    assert lib.moat_lut_softmax(FAKE, 0, 2, 1000, FAKE, 32768, step, None, None) == I  # no output
+    assert lib.moat_lut_softmax(FAKE, 2, 2, 1000, FAKE, 32768, step, FAKE, None) == I  # int8 logits
+    assert lib.moat_lut_softmax(FAKE, 0, 2, 32769, FAKE, 32768, step, FAKE, None) == I  # row above 32768
+    assert lib.moat_lut_softmax(FAKE, 0, 2, 0, FAKE, 32768, step, FAKE, None) == I
+    assert lib.moat_lut_softmax(FAKE, 0, 2, 1000, FAKE, 32769, step, FAKE, None) == I  # table above 32768
+    assert lib.moat_lut_softmax(FAKE, 0, 2, 1000, FAKE, 1, step, FAKE, None) == I
+    assert lib.moat_lut_softmax(FAKE, 0, 2, 1000, FAKE, 32768, F(0.0), FAKE, None) == I
+    assert lib.moat_lut_softmax(FAKE, 0, 2, 1000, FAKE, 32768, F(float("inf")), FAKE, None) == I
+    assert lib.moat_lut_softmax(ctypes.c_void_p(0x10002), 0, 2, 1000, FAKE, 32768, step, FAKE, None) == I
+    assert lib.moat_lut_softmax(ctypes.c_void_p(0x10004), 3, 2, 1000, FAKE, 32768, step, FAKE, None) == I  # f64: 8 B
+    assert lib.moat_lut_softmax(FAKE, 0, 0, 1000, FAKE, 32768, step, None, None) == _lib.MOAT_OK  # no rows
+    # moat_sample_tokens(x, dtype, n, v, T, top_k, seed, lut, lut_size, step, tokens, logprobs, stream)
+    assert lib.moat_sample_tokens(FAKE, 0, 2, 1000, 0.7, 0, 1, FAKE, 32768, step, FAKE, FAKE, None) == I
+    assert lib.moat_sample_tokens(FAKE, 0, 2, 1000, 0.7, 65, 1, FAKE, 32768, step, FAKE, FAKE, None) == I
+    assert lib.moat_sample_tokens(FAKE, 0, 2, 1000, float("nan"), 50, 1, FAKE, 32768, step, FAKE, FAKE, None) == I
+    assert lib.moat_sample_tokens(FAKE, 0, 2, 1000, 0.7, 50, 1, FAKE, 32768, step, None, FAKE, None) == I
+    assert lib.moat_sample_tokens(FAKE, 0, 2, 1000, 0.7, 50, 1, FAKE, 32768, step, FAKE,
+                                  ctypes.c_void_p(0x10002), None) == I
+    assert lib.moat_sample_tokens(FAKE, 1, 2, 40000, 0.0, 50, 1, FAKE, 32768, step, FAKE, FAKE, None) == I
+    assert lib.moat_lut_lookup(FAKE, -1, FAKE, 32768, step, FAKE, None) == I
+    assert lib.moat_lut_lookup(FAKE, 4, FAKE, 1, step, FAKE, None) == I
+    assert lib.moat_lut_lookup(ctypes.c_void_p(0x10002), 4, FAKE, 32768, step, FAKE, None) == I
+    assert lib.moat_lut_lookup(FAKE, 0, FAKE, 32768, step, FAKE, None) == _lib.MOAT_OK
+
+
+def test_sampling_python_checks_first():
+    import numpy as np
+    from moat_amd import sampling
+    with pytest.raises(ValueError):
+        sampling.ExponentialLUT(size=1)
+    with pytest.raises(ValueError):
+        sampling.ExponentialLUT(range_max=-1.0)
+    with pytest.raises(ValueError):
+        sampling.TokenSampler(top_k=65)
+    with pytest.raises(ValueError):
+        sampling.TokenSampler(exp_lut_size=40000)
+    lut = sampling.ExponentialLUT()
+    assert lut.memory_bytes == 65536 and lut.lut.dtype == np.float16 and lut.size == 32768
 
 
 def test_fused_python_shapes_checked_first():
