@@ -137,9 +137,11 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="k2048_m5504", choices=sorted(CONFIGS) + ["layer_h2048", "quantize_load"],
+    ap.add_argument("--config", default="k2048_m5504",
+                    choices=sorted(CONFIGS) + ["layer_h2048", "quantize_load", "sample_v32000"],
                     help="projection shape; layer_h2048: one decoder layer's 7 projections at N=16; "
-                         "quantize_load: fp16 weights of one layer to INT4 records on the GPU")
+                         "quantize_load: fp16 weights of one layer to INT4 records on the GPU; "
+                         "sample_v32000: token sampling from V=32000 logits, alone and after the INT4 LM head")
     ap.add_argument("--ns", default=None, help="comma-separated N values (default: the config's)")
     ap.add_argument("--algo", type=int, default=0, help="0 auto, 1 dot2, 2 mfma")
     ap.add_argument("--splits", type=int, default=0)
@@ -177,6 +179,8 @@ def main() -> int:
         return run_layer(args)
     if args.config == "quantize_load":
         return run_quantize_load(args)
+    if args.config == "sample_v32000":
+        return run_sample(args)
 
     import torch
     from moat_amd import _lib
@@ -318,6 +322,134 @@ def main() -> int:
                    "algo": args.algo, "splits": args.splits, "batch": args.batch, "finish": args.finish,
                    "front": args.front, "weights": "int4 superblocks (144 B per 256 weights)",
                    "activations": "fp16", "output": "fp32"},
+        "per_n": {str(k): v for k, v in per_n.items()},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+SAMPLE_V = 32000
+SAMPLE_K = 2048
+SAMPLE_T = 0.7  # the coordinator's default temperature (batch_generator.py:190)
+
+
+def run_sample(args) -> int:
+    """Token sampling from LM-head logits, V = 32000, N = 1..32 rows: the
+    sampler alone (greedy and T = 0.7, logits already on the GPU), and one
+    decode step's tail -- the INT4 LM head K=2048 x V=32000 (weight copies
+    rotated) followed by the T = 0.7 sampler.  value = tokens/s of the LM
+    head + sampler over the N sweep; the CPU baseline is the numpy oracle of
+    the reference's sampler on the same logits."""
+    import torch
+    from moat_amd import _lib
+    from moat_amd.dequant import _gemm_into, quantize_to_superblocks
+    from moat_amd.sampling import TokenSampler
+
+    lib = _lib.load()
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    ns = [int(v) for v in args.ns.split(",")] if args.ns else [1, 2, 4, 8, 16, 32]
+    K, V = SAMPLE_K, SAMPLE_V
+    sampler = TokenSampler()
+    table = sampler.exp_lut.table()
+    step = sampler.exp_lut.step_f32
+    rng = np.random.default_rng(1007)
+    w = torch.from_numpy(rng.standard_normal((K, V), dtype=np.float32) * np.float32(0.02)).to(dev)
+    blob0 = quantize_to_superblocks(w)
+    del w
+    copies = max(2, -(-ROTATE_BYTES // blob0.numel()))
+    blobs = [blob0] + [blob0.clone() for _ in range(copies - 1)]
+    xs = {N: torch.from_numpy(np.random.default_rng(2100 + N).standard_normal((N, K), dtype=np.float32)
+                              .astype(np.float16)).to(dev) for N in ns}
+    logits = {N: torch.empty((N, V), dtype=torch.float32, device=dev) for N in ns}
+    toks = {N: torch.empty(N, dtype=torch.int32, device=dev) for N in ns}
+    lps = {N: torch.empty(N, dtype=torch.float32, device=dev) for N in ns}
+    log(f"[bench] sample_v32000: LM head {K}x{V} ({blob0.numel() / 1e6:.2f} MB records, {copies} copies), "
+        f"table {sampler.exp_lut.size} entries")
+    cap = torch.cuda.Stream()
+    cap.wait_stream(torch.cuda.current_stream())
+
+    def sample(N, temp, seed):
+        _lib.check(lib.moat_sample_tokens(logits[N].data_ptr(), _lib.DTYPE_F32, N, V, temp, sampler.top_k, seed,
+                                          table.data_ptr(), sampler.exp_lut.size, step, toks[N].data_ptr(),
+                                          lps[N].data_ptr(), cap.cuda_stream), "sample")
+
+    def head(N, i):
+        _gemm_into(xs[N], blobs[i % copies], logits[N], K, V)
+
+    with torch.cuda.stream(cap):
+        for N in ns:
+            for i in range(2):
+                head(N, i)
+                sample(N, SAMPLE_T, i)
+                sample(N, 0.0, i)
+    torch.cuda.synchronize()
+
+    def capture(fn, calls):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=cap):
+            for c in range(calls):
+                fn(c)
+        torch.cuda.synchronize()
+        return g
+
+    def timed(g, reps):
+        with torch.cuda.stream(cap):
+            g.replay()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(cap)
+            for _ in range(reps):
+                g.replay()
+            e1.record(cap)
+        e1.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / reps  # us per replay
+
+    per_n = {}
+    calls = max(copies, 20)
+    for N in ns:
+        greedy = timed(capture(lambda c: sample(N, 0.0, c), calls), max(2, args.steps // 10)) / calls
+        samp = timed(capture(lambda c: sample(N, SAMPLE_T, c), calls), max(2, args.steps // 10)) / calls
+        pipe = timed(capture(lambda c: (head(N, c), sample(N, SAMPLE_T, c)), copies),
+                     max(2, args.steps // 10)) / copies
+        sbytes = N * V * 4 + N * 2 * sampler.exp_lut.size + 8 * N  # logits, the table per row, outputs
+        per_n[N] = {"sample_us": round(samp, 3), "greedy_us": round(greedy, 3), "lm_head_plus_sample_us": round(pipe, 3),
+                    "tok_s": round(N / pipe * 1e6, 1), "sample_bytes": sbytes,
+                    "sample_gbs": round(sbytes / samp / 1e3, 1)}
+        log(f"[bench] N={N:2d}: sample {samp:7.2f} us  greedy {greedy:7.2f} us  LM head + sample {pipe:7.2f} us  "
+            f"({N / pipe * 1e6:9.0f} tok/s)")
+    total_us = sum(per_n[N]["lm_head_plus_sample_us"] for N in ns)
+    value = sum(ns) / (total_us / 1e6)
+    log(f"[bench] sweep: {total_us:.1f} us, {value:.0f} tok/s (LM head + sampler)")
+    dom = max(ns)
+    roof = {"bound": "hbm", "achieved": per_n[dom]["sample_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(per_n[dom]["sample_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+            "kernel": (f"lut_sample_kernel N={dom}: {per_n[dom]['sample_bytes']} B per call (fp32 logits, the "
+                       f"64 KB table per row, tokens and logs) / {per_n[dom]['sample_us']} us")}
+    cpu = None
+    if not args.no_cpu_baseline:
+        sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+        from oracle import sampling_oracle as S
+        host = logits[16 if 16 in ns else dom].cpu().numpy()
+        t0 = time.perf_counter()
+        rows = 0
+        while time.perf_counter() - t0 < min(args.cpu_budget, 10.0):
+            S.sample_tokens(host, temperature=SAMPLE_T, seed=rows)
+            rows += host.shape[0]
+        dt = time.perf_counter() - t0
+        cpu = {"value": rows / dt, "unit": "tok/s", "cores": 1, "kind": "port",
+               "sample": f"numpy oracle of the reference's sampler (table softmax, top-50, one draw) on "
+                         f"{host.shape[0]}x{V} fp32 logits, repeated for ~10 s; sampling only, no LM head"}
+        log(f"[bench] CPU baseline: {cpu['value']:.1f} tok/s sampled")
+    out = {
+        "metric": "token sampling from LM-head logits: us/call and tok/s of INT4 LM head + sampler at N=1..32",
+        "value": round(value, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": 1,
+        "ms_per_step": round(total_us / 1e3, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic",
+        "config": {"workload": f"LM head K={K} x V={V} (INT4 records) then table-softmax top-50 sampling at "
+                               f"T={SAMPLE_T}, N sweep {ns}", "copies": copies,
+                   "timing": "HIP graph replay, HIP events on the launch stream"},
         "per_n": {str(k): v for k, v in per_n.items()},
         "roofline": roof,
         "cpu_baseline": cpu,
