@@ -180,7 +180,6 @@ def test_sampling_entry_points_validate(lib):
     I = _lib.MOAT_ERR_INVALID
     F = ctypes.c_float
     step = F(10.0 / 32767)
-    ok = dict(dtype=0, n=2, v=1000, lut_size=32768)
     # moat_lut_softmax(x, dtype, n, v, lut, lut_size, step, probs, stream)
     assert lib.moat_lut_softmax(FAKE, 0, 2, 1000, FAKE, 32768, step, None, None) == I  # no output
     assert lib.moat_lut_softmax(FAKE, 2, 2, 1000, FAKE, 32768, step, FAKE, None) == I  # int8 logits
