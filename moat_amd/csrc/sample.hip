@@ -88,6 +88,27 @@ __device__ __forceinline__ float conv(uint16_t r) { return h2f(r); }
 __device__ __forceinline__ float scale_conv(float r, double t) { return __fdiv_rn(r, (float)t); }
 __device__ __forceinline__ float scale_conv(double r, double t) { return (float)__ddiv_rn(r, t); }
 __device__ __forceinline__ float scale_conv(uint16_t r, double t) { return h2f(f2h(__fdiv_rn(h2f(r), (float)t))); }
+// a / b rounded to nearest even from r = RN(1 / b), b > 0, by Markstein's FMA
+// sequence: q0 = RN(a r), rem = a - q0 b (exact), q = RN(q0 + rem r).  It is
+// the correctly rounded quotient when a and q0 are 0 or in [2^-100, 2^100]
+// (tests/test_markstein_division.py checks it against IEEE division over a
+// whole binade of dividends for the table step, sums, hard and random
+// divisor significands); it can miss by an ulp when the quotient is
+// subnormal and gives NaN when it overflows.  `fast` says whether a and q0 are in the range.  Used where
+// neither case changes the result: the table index (a quotient below 1 is
+// index 0, one above 2^100 the last index) and e / sum (always in range).
+__device__ __forceinline__ float div_markstein(float a, float b, float r, bool& fast) {
+  asm volatile("" : "+v"(a));  // a converted on its own (no mixed-precision fma)
+  const float q0 = a * r;
+  const float rem = __builtin_fmaf(-q0, b, a);
+  const float aa = fabsf(a), aq = fabsf(q0);
+  fast = aa == 0.f || (aa >= 0x1p-100f && aa <= 0x1p100f && aq >= 0x1p-100f && aq <= 0x1p100f);
+  float q = __builtin_fmaf(rem, r, q0);
+  // the float32 quotient as such: fused with a following fp16 conversion
+  // (v_fma_mixlo_f16) it would be rounded once, to fp16, instead of twice
+  asm volatile("" : "+v"(q));
+  return q;
+}
 // raw value for an argmax (exact in double for every input dtype)
 __device__ __forceinline__ double raw_d(float r) { return (double)r; }
 __device__ __forceinline__ double raw_d(double r) { return r; }
@@ -362,15 +383,19 @@ __global__ void __launch_bounds__(kSThreads) lut_sample_kernel(const T* __restri
   for (int j = 0; j < kSPer; ++j) raw[j] = xr[min(t + j * kSThreads, v - 1)];
   for (int i = t; i < lut_size; i += kSThreads) S.lut[i] = lut[i];
 
-  float xs[kSPer];  // scaled values as float32, -inf past the row's end
+  // scaled values as float32, -inf past the row's end (x / T divides in full:
+  // arbitrary logits can put the quotient where Markstein's sequence is not
+  // exact)
+  float xs[kSPer];
+#pragma unroll
+  for (int j = 0; j < kSPer; ++j) xs[j] = kScaled ? scale_conv(raw[j], temp) : conv(raw[j]);
   float mx = -INFINITY;
   bool nan_seen = false;
 #pragma unroll
   for (int j = 0; j < kSPer; ++j) {
     const bool ok = t + j * kSThreads < v;
-    const float s = kScaled ? scale_conv(raw[j], temp) : conv(raw[j]);
-    nan_seen = nan_seen || (ok && isnan(s));
-    xs[j] = ok ? s : -INFINITY;
+    nan_seen = nan_seen || (ok && isnan(xs[j]));
+    xs[j] = ok ? xs[j] : -INFINITY;
     mx = fmaxf(mx, xs[j]);
   }
   const float wm = wave_max(nan_seen ? NAN : mx);
@@ -450,11 +475,16 @@ __global__ void __launch_bounds__(kSThreads) lut_sample_kernel(const T* __restri
   const float top = (float)(lut_size - 1);
   uint16_t* const my_e = S.e + epos(t);
   {
+    // |x - max| / step by Markstein's sequence: outside its range the
+    // quotient is either below 1 (index 0 either way) or far above the last
+    // index (NaN or huge here, clamped to it)
+    const float rs = __fdiv_rn(1.0f, step);
     uint16_t tv[kSPer];
 #pragma unroll
     for (int j = 0; j < kSPer; ++j) {
-      const float a = __fdiv_rn(fabsf(xs[j] - m), step);
-      tv[j] = S.lut[lut_size - 1 - (int)fminf(a, top)];
+      bool fast;
+      const float a = div_markstein(fabsf(xs[j] - m), step, rs, fast);
+      tv[j] = S.lut[lut_size - 1 - (int)(a == a ? fminf(a, top) : top)];
     }
 #pragma unroll
     for (int j = 0; j < kSPer; ++j) my_e[1088 * j] = tv[j];
@@ -474,17 +504,21 @@ __global__ void __launch_bounds__(kSThreads) lut_sample_kernel(const T* __restri
     return;
   }
 
-  // 4. probabilities (each thread rewrites its own slots)
+  // 4. probabilities (each thread rewrites its own slots); e / sum by
+  // Markstein's sequence, always in its range (e is 0 or at least 2^-24 and
+  // at most 1; 1 <= sum <= 32768, the maximum's table value being 1)
+  const float rsum = __fdiv_rn(1.0f, sum);
+  bool fast;
   if (mode == kModeProbs) {
 #pragma unroll
     for (int j = 0; j < kSPer; ++j) {
       const int i = t + j * kSThreads;
-      if (i < v) probs[(int64_t)row * v + i] = f2h(__fdiv_rn(h2f(my_e[1088 * j]), sum));
+      if (i < v) probs[(int64_t)row * v + i] = f2h(div_markstein(h2f(my_e[1088 * j]), sum, rsum, fast));
     }
     return;
   }
 #pragma unroll
-  for (int j = 0; j < kSPer; ++j) my_e[1088 * j] = f2h(__fdiv_rn(h2f(my_e[1088 * j]), sum));
+  for (int j = 0; j < kSPer; ++j) my_e[1088 * j] = f2h(div_markstein(h2f(my_e[1088 * j]), sum, rsum, fast));
 
   // 5. the k largest p, index order among equal p: each wave takes the first
   // k entries of its own 2048 (thread t re-reads elements 32t .. 32t+31 of
