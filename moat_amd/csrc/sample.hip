@@ -524,7 +524,8 @@ __global__ void __launch_bounds__(kSThreads) lut_sample_kernel(const T* __restri
   // k entries of its own 2048 (thread t re-reads elements 32t .. 32t+31 of
   // the row from LDS, so that a wave's entries are in index order); the k
   // first of the whole row are among those 16 lists, which wave 0 selects
-  // from.  Keys are encoded as the fp16 bits + 1 (0: past the row's end).
+  // from.  Keys are encoded as the fp16 bits + 1 (0: past the row's end);
+  // list entries are key << 16 | index.
   __syncthreads();
   const uint32_t kk = (uint32_t)min(top_k, v);
   {
@@ -540,13 +541,68 @@ __global__ void __launch_bounds__(kSThreads) lut_sample_kernel(const T* __restri
         ek[4 * q4 + h].y = i0 + 1 < v ? (unsigned short)((ws[h] >> 16) + 1) : (unsigned short)0;
       }
     }
-    uint32_t take = wave_select<kSPer>(ek, kk);
+    // lower bound of the wave's k-th largest key: the k-th largest of the 64
+    // lane maxima (k lanes each hold a key at least that large), by ballots
+    us2 m2 = ek[0];
+#pragma unroll
+    for (int h = 1; h < kSPer / 2; ++h) m2 = __builtin_elementwise_max(m2, ek[h]);
+    const uint32_t lmax = max((uint32_t)m2.x, (uint32_t)m2.y);
+    uint32_t lb = 0;
+    for (int bit = 14; bit >= 0; --bit) {
+      const uint32_t c = lb | (1u << bit);
+      if ((uint32_t)__popcll(__ballot(lmax >= c)) >= kk) lb = c;
+    }
+    lb = max(lb, 1u);
+    uint32_t cm = 0;  // this lane's candidates: keys >= lb
+#pragma unroll
+    for (int h = 0; h < kSPer / 2; ++h) {
+      cm |= (ek[h].x >= lb ? 1u : 0u) << (2 * h);
+      cm |= (ek[h].y >= lb ? 1u : 0u) << (2 * h + 1);
+    }
+    uint32_t n_cand;
+    uint32_t at = wave_prefix((uint32_t)__popc(cm), n_cand);
+    uint32_t take;
+    uint32_t pos[4];
+    if (n_cand <= 256) {
+      // compact the candidates (in index order) into this wave's 256-entry
+      // list (the sum's chain area, free now), then select exactly among them
+      uint32_t* list = reinterpret_cast<uint32_t*>(&S.chain[0][0][0]) + 256 * wv;
+      for (uint32_t mm = cm; mm;) {
+        const int jj = __ffs(mm) - 1;
+        mm &= mm - 1;
+        const int i = kSPer * t + jj;
+        list[at++] = ((uint32_t)S.e[epos(i)] + 1u) << 16 | (uint32_t)i;
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+      us2 ck[2];
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        const uint32_t e = 4 * lane + h;
+        const uint32_t val = e < n_cand ? list[e] : 0u;
+        pos[h] = val;
+        if (h & 1) ck[h >> 1].y = (unsigned short)(val >> 16);
+        else ck[h >> 1].x = (unsigned short)(val >> 16);
+      }
+      take = wave_select<4>(ck, kk);
+    } else {
+      // many equal keys near the top (e.g. a flat row): search all 32 per lane
+      take = wave_select<kSPer>(ek, kk);
+    }
     uint32_t total;
-    uint32_t at = wave_prefix((uint32_t)__popc(take), total);
-    while (take) {  // few lanes hold any of the wave's k entries
-      const int jj = __ffs(take) - 1;
-      take &= take - 1;
-      S.wc[wv][at++] = kSPer * t + jj;
+    at = wave_prefix((uint32_t)__popc(take), total);
+    if (n_cand <= 256) {
+#pragma unroll
+      for (int h = 0; h < 4; ++h)
+        if ((take >> h) & 1u) S.wc[wv][at++] = (int)pos[h];
+    } else {
+      while (take) {  // few lanes hold any of the wave's k entries
+        const int jj = __ffs(take) - 1;
+        take &= take - 1;
+        const int i = kSPer * t + jj;
+        S.wc[wv][at++] = (int)(((uint32_t)S.e[epos(i)] + 1u) << 16 | (uint32_t)i);
+      }
     }
     if (lane == 0) S.wcount[wv] = total;
   }
@@ -555,13 +611,13 @@ __global__ void __launch_bounds__(kSThreads) lut_sample_kernel(const T* __restri
   {
     // wave 0: the 16 lists, 16 entries per lane, in index order
     us2 ek[8];
-    int idx[16];
+    int ent[16];
+    const uint32_t cnt = S.wcount[lane >> 2];  // a lane's 16 entries lie in list lane / 4
 #pragma unroll
     for (int h = 0; h < 16; ++h) {
-      const int e = 16 * lane + h, w = e >> 6, p = e & 63;
-      const bool ok = (uint32_t)p < S.wcount[w];
-      idx[h] = ok ? S.wc[w][p] : 0;
-      const unsigned short k = ok ? (unsigned short)(S.e[epos(idx[h])] + 1) : (unsigned short)0;
+      const int p = (16 * lane + h) & 63;
+      ent[h] = (uint32_t)p < cnt ? S.wc[lane >> 2][p] : 0;
+      const unsigned short k = (unsigned short)((uint32_t)ent[h] >> 16);
       if (h & 1) ek[h >> 1].y = k;
       else ek[h >> 1].x = k;
     }
@@ -570,7 +626,7 @@ __global__ void __launch_bounds__(kSThreads) lut_sample_kernel(const T* __restri
     uint32_t at = wave_prefix((uint32_t)__popc(take), total);
 #pragma unroll
     for (int h = 0; h < 16; ++h)
-      if ((take >> h) & 1) S.cand[at++] = idx[h];
+      if ((take >> h) & 1) S.cand[at++] = ent[h];
     // the wave's LDS writes before its reads of them
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     __builtin_amdgcn_wave_barrier();
@@ -581,8 +637,9 @@ __global__ void __launch_bounds__(kSThreads) lut_sample_kernel(const T* __restri
   // takes rank r; their sum in numpy's order; the draw
   const int kc = (int)kk;
   const bool live = lane < kc;
-  const int mi = live ? S.cand[lane] : 0;
-  const int mk = live ? (int)S.e[epos(mi)] : -1;
+  const uint32_t ce = live ? (uint32_t)S.cand[lane] : 0u;
+  const int mi = (int)(ce & 0xFFFFu);
+  const int mk = live ? (int)(ce >> 16) - 1 : -1;  // the fp16 bits of p
   int rank = 0;
   for (int o = 0; o < kc; ++o) {
     const int ok = rl(mk, o), oi = rl(mi, o);
