@@ -138,10 +138,11 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="k2048_m5504",
-                    choices=sorted(CONFIGS) + ["layer_h2048", "quantize_load", "sample_v32000"],
+                    choices=sorted(CONFIGS) + ["layer_h2048", "quantize_load"] + sorted(SAMPLE_CONFIGS),
                     help="projection shape; layer_h2048: one decoder layer's 7 projections at N=16; "
                          "quantize_load: fp16 weights of one layer to INT4 records on the GPU; "
-                         "sample_v32000: token sampling from V=32000 logits, alone and after the INT4 LM head")
+                         "sample_v32000 / sample_v128256: token sampling from V=32000 (K=2048 LM head) or "
+                         "V=128256 (K=4096) logits, alone and after the INT4 LM head")
     ap.add_argument("--ns", default=None, help="comma-separated N values (default: the config's)")
     ap.add_argument("--algo", type=int, default=0, help="0 auto, 1 dot2, 2 mfma")
     ap.add_argument("--splits", type=int, default=0)
@@ -179,7 +180,7 @@ def main() -> int:
         return run_layer(args)
     if args.config == "quantize_load":
         return run_quantize_load(args)
-    if args.config == "sample_v32000":
+    if args.config in SAMPLE_CONFIGS:
         return run_sample(args)
 
     import torch
@@ -330,18 +331,19 @@ def main() -> int:
     return 0
 
 
-SAMPLE_V = 32000
-SAMPLE_K = 2048
+# name -> (LM head K, vocabulary V): a 32000-token vocabulary after a hidden
+# size of 2048, and Llama-3's 128256 tokens after 4096
+SAMPLE_CONFIGS = {"sample_v32000": (2048, 32000), "sample_v128256": (4096, 128256)}
 SAMPLE_T = 0.7  # the coordinator's default temperature (batch_generator.py:190)
 
 
 def run_sample(args) -> int:
-    """Token sampling from LM-head logits, V = 32000, N = 1..32 rows: the
-    sampler alone (greedy and T = 0.7, logits already on the GPU), and one
-    decode step's tail -- the INT4 LM head K=2048 x V=32000 (weight copies
-    rotated) followed by the T = 0.7 sampler.  value = tokens/s of the LM
-    head + sampler over the N sweep; the CPU baseline is the numpy oracle of
-    the reference's sampler on the same logits."""
+    """Token sampling from LM-head logits, N = 1..32 rows: the sampler alone
+    (greedy and T = 0.7, logits already on the GPU), and one decode step's
+    tail -- the INT4 LM head K x V (weight copies rotated) followed by the
+    T = 0.7 sampler.  value = tokens/s of the LM head + sampler over the N
+    sweep; the CPU baseline is the numpy oracle of the reference's sampler on
+    the same logits."""
     import torch
     from moat_amd import _lib
     from moat_amd.dequant import _gemm_into, quantize_to_superblocks
@@ -351,7 +353,7 @@ def run_sample(args) -> int:
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     ns = [int(v) for v in args.ns.split(",")] if args.ns else [1, 2, 4, 8, 16, 32]
-    K, V = SAMPLE_K, SAMPLE_V
+    K, V = SAMPLE_CONFIGS[args.config]
     sampler = TokenSampler()
     table = sampler.exp_lut.table()
     step = sampler.exp_lut.step_f32
@@ -366,7 +368,9 @@ def run_sample(args) -> int:
     logits = {N: torch.empty((N, V), dtype=torch.float32, device=dev) for N in ns}
     toks = {N: torch.empty(N, dtype=torch.int32, device=dev) for N in ns}
     lps = {N: torch.empty(N, dtype=torch.float32, device=dev) for N in ns}
-    log(f"[bench] sample_v32000: LM head {K}x{V} ({blob0.numel() / 1e6:.2f} MB records, {copies} copies), "
+    ws_bytes = int(lib.moat_sample_workspace_size(max(ns), V))
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)  # row counters start at zero
+    log(f"[bench] {args.config}: LM head {K}x{V} ({blob0.numel() / 1e6:.2f} MB records, {copies} copies), "
         f"table {sampler.exp_lut.size} entries")
     cap = torch.cuda.Stream()
     cap.wait_stream(torch.cuda.current_stream())
@@ -374,7 +378,7 @@ def run_sample(args) -> int:
     def sample(N, temp, seed):
         _lib.check(lib.moat_sample_tokens(logits[N].data_ptr(), _lib.DTYPE_F32, N, V, temp, sampler.top_k, seed,
                                           table.data_ptr(), sampler.exp_lut.size, step, toks[N].data_ptr(),
-                                          lps[N].data_ptr(), cap.cuda_stream), "sample")
+                                          lps[N].data_ptr(), ws.data_ptr(), ws_bytes, cap.cuda_stream), "sample")
 
     def head(N, i):
         _gemm_into(xs[N], blobs[i % copies], logits[N], K, V)
@@ -413,7 +417,7 @@ def run_sample(args) -> int:
         samp = timed(capture(lambda c: sample(N, SAMPLE_T, c), calls), max(2, args.steps // 10)) / calls
         pipe = timed(capture(lambda c: (head(N, c), sample(N, SAMPLE_T, c)), copies),
                      max(2, args.steps // 10)) / copies
-        sbytes = N * V * 4 + N * 2 * sampler.exp_lut.size + 8 * N  # logits, the table per row, outputs
+        sbytes = N * V * 4 + 2 * sampler.exp_lut.size + 8 * N  # logits, the table, tokens and logs
         per_n[N] = {"sample_us": round(samp, 3), "greedy_us": round(greedy, 3), "lm_head_plus_sample_us": round(pipe, 3),
                     "tok_s": round(N / pipe * 1e6, 1), "sample_bytes": sbytes,
                     "sample_gbs": round(sbytes / samp / 1e3, 1)}
@@ -425,8 +429,8 @@ def run_sample(args) -> int:
     dom = max(ns)
     roof = {"bound": "hbm", "achieved": per_n[dom]["sample_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(per_n[dom]["sample_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
-            "kernel": (f"lut_sample_kernel N={dom}: {per_n[dom]['sample_bytes']} B per call (fp32 logits, the "
-                       f"64 KB table per row, tokens and logs) / {per_n[dom]['sample_us']} us")}
+            "kernel": (f"sampler (4 launches) N={dom}: {per_n[dom]['sample_bytes']} B per call (fp32 logits, "
+                       f"the 64 KB table, tokens and logs) / {per_n[dom]['sample_us']} us")}
     cpu = None
     if not args.no_cpu_baseline:
         sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))

@@ -253,10 +253,30 @@ int32_t moat_int4_to_f16(const void* src, int32_t src_dtype, int64_t n, uint16_t
  * and the table softmax it calls, antigravity-engine/src/attention.py:97-135).
  *
  * `lut_f16` is the exp table of ExponentialLUT (attention.py:32-58): lut_size
- * fp16 values of exp over [-range_max, 0], 2 <= lut_size <= 32768; `step` is
+ * fp16 values of exp over [-range_max, 0], 2 <= lut_size <= 2^24; `step` is
  * range_max / (lut_size - 1) rounded to float32.  Logits are [n][v] of dtype
- * F32, F16 or F64, 1 <= v <= 32768, one row per workgroup.
+ * F32, F16 or F64, 0 <= n <= 2^22, 1 <= v <= 524288 (up to 64 chunks of 8192
+ * logits, one workgroup each).
  *
+ * Both calls take a device workspace, 256-byte aligned, of at least the
+ * bytes the size calls below give (sampling: about 2 v + 600 bytes per row;
+ * softmax: about 600 bytes per 8192 logits, its table values going to the
+ * output buffer; MOAT_ERR_WORKSPACE when missing or short).  It starts with
+ * one counter word per row, through which the last of a row's workgroups
+ * (one per 8192 logits) takes over the row: zero-fill the workspace once
+ * before first use (e.g. with moat_int4_workspace_clear); every call leaves
+ * the counters at zero again, so one workspace serves calls of any shape.
+ * Calls that share a workspace must not overlap; use a different workspace
+ * from the GEMM's.
+ */
+
+/* Workspace bytes of a moat_sample_tokens / moat_lut_softmax call over n rows
+ * of v logits (0 when n is 0; -1 for sizes outside the limits above).  No
+ * counterpart in the reference, whose numpy sampler allocates as it goes. */
+int64_t moat_sample_workspace_size(int32_t n, int32_t v);
+int64_t moat_lut_softmax_workspace_size(int32_t n, int32_t v);
+
+/*
  * moat_lut_softmax: probs_f16[n][v] = safe_softmax_lut(x) along each row:
  * row max (f32), table index size-1-trunc(min(|x - max| / step, size-1)),
  * numpy's float32 pairwise sum of the table values, fp16(e / sum).  A row
@@ -264,7 +284,8 @@ int32_t moat_int4_to_f16(const void* src, int32_t src_dtype, int64_t n, uint16_t
  * there) gives NaN.
  */
 int32_t moat_lut_softmax(const void* x, int32_t dtype, int32_t n, int32_t v, const uint16_t* lut_f16,
-                         int32_t lut_size, float step, uint16_t* probs_f16, hipStream_t stream);
+                         int32_t lut_size, float step, uint16_t* probs_f16, void* workspace,
+                         int64_t workspace_bytes, hipStream_t stream);
 
 /*
  * moat_sample_tokens: temperature <= 0: greedy, tokens[r] = np.argmax(row r)
@@ -282,7 +303,8 @@ int32_t moat_lut_softmax(const void* x, int32_t dtype, int32_t n, int32_t v, con
  */
 int32_t moat_sample_tokens(const void* logits, int32_t dtype, int32_t n, int32_t v, double temperature,
                            int32_t top_k, uint64_t seed, const uint16_t* lut_f16, int32_t lut_size,
-                           float step, int32_t* tokens, float* logprobs, hipStream_t stream);
+                           float step, int32_t* tokens, float* logprobs, void* workspace,
+                           int64_t workspace_bytes, hipStream_t stream);
 
 /* ExponentialLUT.lookup (attention.py:60-85): out_f16[i] =
  * lut[size-1-trunc(min(|x[i]| / step, size-1))] for float32 x (NaN -> NaN). */

@@ -1,5 +1,5 @@
 """Device plumbing: numpy/torch inputs to device tensors, pointers, streams,
-and the per-stream GEMM workspace.  torch provides memory and streams only;
+and the per-stream workspaces.  torch provides memory and streams only;
 all arithmetic of the path runs in libmoat_int4.so."""
 
 from __future__ import annotations
@@ -83,7 +83,7 @@ def out_like(t: torch.Tensor, want_tensor: bool):
 
 class _Workspaces:
     """One zero-initialised workspace per (device, stream), grown on demand.
-    The GEMM kernels leave its counter words at zero after every call."""
+    The kernels leave its counter words at zero after every call."""
 
     def __init__(self) -> None:
         self._lock = threading.Lock()
@@ -105,4 +105,5 @@ class _Workspaces:
             return buf
 
 
-workspaces = _Workspaces()
+workspaces = _Workspaces()  # GEMM calls
+sample_workspaces = _Workspaces()  # sampling calls (their own: other counter words)

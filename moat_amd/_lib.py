@@ -61,9 +61,11 @@ SIGNATURES = {
     "moat_int4_lut_gather": (_I32, [_P, _I64, _I32, _P, _I64, _I32, _P, _P]),
     "moat_int4_any_negative": (_I32, [_P, _I64, _P, _P]),
     "moat_int4_to_f16": (_I32, [_P, _I32, _I64, _P, _P]),
-    "moat_lut_softmax": (_I32, [_P, _I32, _I32, _I32, _P, _I32, ctypes.c_float, _P, _P]),
+    "moat_sample_workspace_size": (_I64, [_I32, _I32]),
+    "moat_lut_softmax_workspace_size": (_I64, [_I32, _I32]),
+    "moat_lut_softmax": (_I32, [_P, _I32, _I32, _I32, _P, _I32, ctypes.c_float, _P, _P, _I64, _P]),
     "moat_sample_tokens": (_I32, [_P, _I32, _I32, _I32, ctypes.c_double, _I32, ctypes.c_uint64, _P, _I32,
-                                  ctypes.c_float, _P, _P, _P]),
+                                  ctypes.c_float, _P, _P, _P, _I64, _P]),
     "moat_lut_lookup": (_I32, [_P, _I64, _P, _I32, ctypes.c_float, _P, _P]),
 }
 

@@ -33,9 +33,11 @@ int gemm_fused_groups(int mode, int mats, int m);
 hipError_t launch_gemm_fused(int mode, const uint16_t* x, const uint8_t* const* sbs, float* const* ys, uint16_t* h,
                              int mats, int n, int k, int m, int wgs, int depth, int finish, float* partials,
                              hipStream_t stream);
+int sample_max_vocab();
+int64_t sample_workspace_bytes(int n, int v, bool with_e);
 hipError_t launch_lut_sample(const void* x, int dtype, int n, int v, double temp, int scaled, const uint16_t* lut,
                              int lut_size, float step, int mode, int top_k, uint64_t seed, int32_t* tokens,
-                             float* logprobs, uint16_t* probs, hipStream_t st);
+                             float* logprobs, uint16_t* probs, void* workspace, hipStream_t st);
 hipError_t launch_lut_lookup(const float* x, int64_t n, const uint16_t* lut, int lut_size, float step, uint16_t* out,
                              hipStream_t st);
 hipError_t launch_gemm(int algo, const uint16_t* x, const uint8_t* sb, float* y, int n, int k, int m, int splits,
@@ -262,17 +264,33 @@ int32_t run_fused(int mode, const uint16_t* x, const uint8_t* const* sbs, float*
                                            partials, stream));
 }
 
-// Shared checks of the sampling entry points: dtype, 1 <= v <= 32768 (a row
-// in one workgroup), table of 2..32768 fp16 entries, positive finite step.
+// Row count (a row's workgroup index times 1024 threads fits 32 bits) and
+// vocabulary (64 chunks of 8192 logits) of the sampling calls.
+bool sample_sizes_ok(int32_t n, int32_t v) {
+  return n >= 0 && n <= (1 << 22) && v >= 1 && v <= moat::sample_max_vocab();
+}
+
+// Shared checks of the sampling entry points: dtype, 1 <= v <= 524288 (64
+// chunks of 8192 logits), table of 2..2^24 fp16 entries (indices exact in
+// float32), positive finite step, at most 2^22 rows (a row's workgroup
+// index times 1024 threads fits 32 bits).
 bool sample_args_ok(const void* x, int32_t dtype, int32_t n, int32_t v, const uint16_t* lut, int32_t lut_size,
                     float step) {
   if (dtype != MOAT_DTYPE_F32 && dtype != MOAT_DTYPE_F16 && dtype != MOAT_DTYPE_F64) return false;
-  if (n < 0 || v < 1 || v > 32768 || lut_size < 2 || lut_size > 32768) return false;
+  if (!sample_sizes_ok(n, v)) return false;
+  if (lut_size < 2 || lut_size > (1 << 24)) return false;
   if (!(step > 0.f) || step == INFINITY) return false;
   if (n == 0) return true;
   const uintptr_t elem = dtype == MOAT_DTYPE_F32 ? 4 : dtype == MOAT_DTYPE_F16 ? 2 : 8;
   return x && lut && aligned(x, elem) && aligned(lut, 2);
 }
+
+// The sampling workspace: present, large enough and 256-byte aligned.
+bool sample_ws_ok(int32_t n, int32_t v, bool with_e, const void* workspace, int64_t workspace_bytes) {
+  return n == 0 || (workspace && aligned(workspace, 256) &&
+                    workspace_bytes >= moat::sample_workspace_bytes(n, v, with_e));
+}
+
 
 int sample_dtype(int32_t dtype) { return dtype == MOAT_DTYPE_F32 ? 0 : dtype == MOAT_DTYPE_F16 ? 1 : 2; }
 
@@ -461,20 +479,32 @@ int32_t moat_int4_to_f16(const void* src, int32_t src_dtype, int64_t n, uint16_t
 
 // ---- token sampling ----
 
+int64_t moat_sample_workspace_size(int32_t n, int32_t v) {
+  return sample_sizes_ok(n, v) ? moat::sample_workspace_bytes(n, v, true) : -1;
+}
+
+int64_t moat_lut_softmax_workspace_size(int32_t n, int32_t v) {
+  return sample_sizes_ok(n, v) ? moat::sample_workspace_bytes(n, v, false) : -1;
+}
+
 int32_t moat_lut_softmax(const void* x, int32_t dtype, int32_t n, int32_t v, const uint16_t* lut_f16,
-                         int32_t lut_size, float step, uint16_t* probs_f16, hipStream_t stream) {
+                         int32_t lut_size, float step, uint16_t* probs_f16, void* workspace, int64_t workspace_bytes,
+                         hipStream_t stream) {
   if (!sample_args_ok(x, dtype, n, v, lut_f16, lut_size, step)) return MOAT_ERR_INVALID;
   if (n > 0 && (!probs_f16 || !aligned(probs_f16, 2))) return MOAT_ERR_INVALID;
+  if (!sample_ws_ok(n, v, false, workspace, workspace_bytes)) return MOAT_ERR_WORKSPACE;
   return status_of(moat::launch_lut_sample(x, sample_dtype(dtype), n, v, 1.0, 0, lut_f16, lut_size, step, 0, 1, 0,
-                                           nullptr, nullptr, probs_f16, stream));
+                                           nullptr, nullptr, probs_f16, workspace, stream));
 }
 
 int32_t moat_sample_tokens(const void* logits, int32_t dtype, int32_t n, int32_t v, double temperature,
                            int32_t top_k, uint64_t seed, const uint16_t* lut_f16, int32_t lut_size, float step,
-                           int32_t* tokens, float* logprobs, hipStream_t stream) {
+                           int32_t* tokens, float* logprobs, void* workspace, int64_t workspace_bytes,
+                           hipStream_t stream) {
   if (!sample_args_ok(logits, dtype, n, v, lut_f16, lut_size, step)) return MOAT_ERR_INVALID;
   if (!(temperature == temperature) || top_k < 1 || top_k > 64) return MOAT_ERR_INVALID;
   if (n > 0 && (!tokens || !logprobs || !aligned(tokens, 4) || !aligned(logprobs, 4))) return MOAT_ERR_INVALID;
+  if (!sample_ws_ok(n, v, true, workspace, workspace_bytes)) return MOAT_ERR_WORKSPACE;
   const bool greedy = temperature <= 0.0;
   // logits / max(T, 1e-5) with T rounded to the logits' dtype first (numpy's
   // array / Python float)
@@ -482,7 +512,8 @@ int32_t moat_sample_tokens(const void* logits, int32_t dtype, int32_t n, int32_t
   if (dtype == MOAT_DTYPE_F32) t = (double)(float)t;
   if (dtype == MOAT_DTYPE_F16) t = (double)(_Float16)t;
   return status_of(moat::launch_lut_sample(logits, sample_dtype(dtype), n, v, t, greedy ? 0 : 1, lut_f16, lut_size,
-                                           step, greedy ? 1 : 2, top_k, seed, tokens, logprobs, nullptr, stream));
+                                           step, greedy ? 1 : 2, top_k, seed, tokens, logprobs, nullptr, workspace,
+                                           stream));
 }
 
 int32_t moat_lut_lookup(const float* x, int64_t n, const uint16_t* lut_f16, int32_t lut_size, float step,

@@ -13,8 +13,8 @@ uses:
   greedy at temperature <= 0, otherwise one draw per row from the 50 most
   probable tokens of the table softmax of logits / T.
 
-All arithmetic runs in ``libmoat_int4.so`` (one workgroup per row, V up to
-32768).  Where the reference leaves a choice open the GPU fixes it: the top-k
+All arithmetic runs in ``libmoat_int4.so`` (one workgroup per 8192-logit
+chunk of a row, V up to 524288).  Where the reference leaves a choice open the GPU fixes it: the top-k
 set and its order are (probability descending, index ascending) -- the
 reference takes ``np.argpartition``'s order -- and row r's uniform draw comes
 from a counter-based generator keyed by ``seed`` (drawn from numpy's global
@@ -36,9 +36,10 @@ import torch
 from . import _device as D
 from . import _lib
 
-MAX_VOCAB = 32768  # logits per row (one workgroup holds a row)
-MAX_TABLE = 32768  # table entries the softmax kernels hold in LDS
+MAX_VOCAB = 64 * 8192  # logits per row: 64 chunks of numpy's 8192-element sum pieces
+MAX_TABLE = 1 << 24  # table entries (indices exact in float32)
 MAX_TOP_K = 64
+_MAX_ROWS = 1 << 22  # rows per call
 DEFAULT_TOP_K = 50  # batch_generator.py:241
 
 _DTYPES = {torch.float32: _lib.DTYPE_F32, torch.float16: _lib.DTYPE_F16, torch.float64: _lib.DTYPE_F64}
@@ -98,6 +99,16 @@ def _logits_dtype(t: torch.Tensor) -> torch.Tensor:
     return t if t.dtype in _DTYPES else t.to(torch.float64)
 
 
+def _workspace(n: int, v: int, softmax: bool = False):
+    """The calling stream's sampling workspace for n rows of v logits."""
+    lib = _lib.load()
+    nbytes = int((lib.moat_lut_softmax_workspace_size if softmax else lib.moat_sample_workspace_size)(n, v))
+    if nbytes < 0:
+        raise ValueError(f"{n} rows of {v} logits: outside the sampler's limits")
+    ws = D.sample_workspaces.get(nbytes)
+    return ws, (ws.numel() if ws is not None else 0)
+
+
 def _check_table(exp_lut: ExponentialLUT) -> None:
     if exp_lut.size > MAX_TABLE:
         raise ValueError(f"table of {exp_lut.size} entries: the GPU softmax holds at most {MAX_TABLE}")
@@ -106,7 +117,7 @@ def _check_table(exp_lut: ExponentialLUT) -> None:
 def safe_softmax_lut(x, exp_lut: ExponentialLUT, axis: int = -1):
     """Softmax along ``axis`` with the table exp (``attention.py:97-135``):
     float32 row max, table lookup of x - max, numpy's float32 sum, fp16
-    quotient.  At most 32768 values along ``axis``."""
+    quotient.  At most 524288 values along ``axis``."""
     _check_table(exp_lut)
     host = not (D.is_tensor(x) and x.is_cuda)
     t = _logits_dtype(D.to_device(x))
@@ -120,9 +131,14 @@ def safe_softmax_lut(x, exp_lut: ExponentialLUT, axis: int = -1):
         raise ValueError(f"{v} values along the softmax axis: at most {MAX_VOCAB}")
     rows = t.numel() // v
     out = torch.empty(t.shape, dtype=torch.float16, device=t.device)
-    _lib.check(_lib.load().moat_lut_softmax(D.ptr(t), _DTYPES[t.dtype], rows, v, D.ptr(exp_lut.table()),
-                                            exp_lut.size, exp_lut.step_f32, D.ptr(out), D.stream()),
-               "safe_softmax_lut")
+    flat_in, flat_out = t.reshape(rows, v), out.reshape(rows, v)
+    for r0 in range(0, rows, _MAX_ROWS):
+        r1 = min(rows, r0 + _MAX_ROWS)
+        ws, ws_bytes = _workspace(r1 - r0, v, softmax=True)
+        _lib.check(_lib.load().moat_lut_softmax(D.ptr(flat_in[r0:r1]), _DTYPES[t.dtype], r1 - r0, v,
+                                                D.ptr(exp_lut.table()), exp_lut.size, exp_lut.step_f32,
+                                                D.ptr(flat_out[r0:r1]), D.ptr(ws), ws_bytes, D.stream()),
+                   "safe_softmax_lut")
     out = torch.movedim(out, -1, axis)
     return D.to_host(out.contiguous()) if host else out
 
@@ -154,10 +170,12 @@ class TokenSampler:
             seed = int(np.random.randint(0, 2 ** 63 - 1, dtype=np.int64))
         tokens = torch.empty(n, dtype=torch.int32, device=t.device)
         logprobs = torch.empty(n, dtype=torch.float32, device=t.device)
+        ws, ws_bytes = _workspace(n, v)
         _lib.check(_lib.load().moat_sample_tokens(D.ptr(t), _DTYPES[t.dtype], n, v, temperature, self.top_k,
                                                   int(seed) & (2 ** 64 - 1), D.ptr(self.exp_lut.table()),
                                                   self.exp_lut.size, self.exp_lut.step_f32, D.ptr(tokens),
-                                                  D.ptr(logprobs), D.stream()), "sample_tokens")
+                                                  D.ptr(logprobs), D.ptr(ws), ws_bytes, D.stream()),
+                   "sample_tokens")
         if temperature <= 0.0:
             tokens, logprobs = tokens.to(torch.int64), logprobs.to(torch.float16)
         if host:

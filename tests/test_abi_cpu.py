@@ -177,29 +177,51 @@ def test_fused_entry_points_validate(lib):
 
 
 def test_sampling_entry_points_validate(lib):
-    I = _lib.MOAT_ERR_INVALID
+    I, W = _lib.MOAT_ERR_INVALID, _lib.MOAT_ERR_WORKSPACE
     F = ctypes.c_float
     step = F(10.0 / 32767)
-    # moat_lut_softmax(x, dtype, n, v, lut, lut_size, step, probs, stream)
-    assert lib.moat_lut_softmax(FAKE, 0, 2, 1000, FAKE, 32768, step, None, None) == I  # no output
-    assert lib.moat_lut_softmax(FAKE, 2, 2, 1000, FAKE, 32768, step, FAKE, None) == I  # int8 logits
-    assert lib.moat_lut_softmax(FAKE, 0, 2, 32769, FAKE, 32768, step, FAKE, None) == I  # row above 32768
-    assert lib.moat_lut_softmax(FAKE, 0, 2, 0, FAKE, 32768, step, FAKE, None) == I
-    assert lib.moat_lut_softmax(FAKE, 0, 2, 1000, FAKE, 32769, step, FAKE, None) == I  # table above 32768
-    assert lib.moat_lut_softmax(FAKE, 0, 2, 1000, FAKE, 1, step, FAKE, None) == I
-    assert lib.moat_lut_softmax(FAKE, 0, 2, 1000, FAKE, 32768, F(0.0), FAKE, None) == I
-    assert lib.moat_lut_softmax(FAKE, 0, 2, 1000, FAKE, 32768, F(float("inf")), FAKE, None) == I
-    assert lib.moat_lut_softmax(ctypes.c_void_p(0x10002), 0, 2, 1000, FAKE, 32768, step, FAKE, None) == I
-    assert lib.moat_lut_softmax(ctypes.c_void_p(0x10004), 3, 2, 1000, FAKE, 32768, step, FAKE, None) == I  # f64: 8 B
-    assert lib.moat_lut_softmax(FAKE, 0, 0, 1000, FAKE, 32768, step, None, None) == _lib.MOAT_OK  # no rows
-    # moat_sample_tokens(x, dtype, n, v, T, top_k, seed, lut, lut_size, step, tokens, logprobs, stream)
-    assert lib.moat_sample_tokens(FAKE, 0, 2, 1000, 0.7, 0, 1, FAKE, 32768, step, FAKE, FAKE, None) == I
-    assert lib.moat_sample_tokens(FAKE, 0, 2, 1000, 0.7, 65, 1, FAKE, 32768, step, FAKE, FAKE, None) == I
-    assert lib.moat_sample_tokens(FAKE, 0, 2, 1000, float("nan"), 50, 1, FAKE, 32768, step, FAKE, FAKE, None) == I
-    assert lib.moat_sample_tokens(FAKE, 0, 2, 1000, 0.7, 50, 1, FAKE, 32768, step, None, FAKE, None) == I
-    assert lib.moat_sample_tokens(FAKE, 0, 2, 1000, 0.7, 50, 1, FAKE, 32768, step, FAKE,
-                                  ctypes.c_void_p(0x10002), None) == I
-    assert lib.moat_sample_tokens(FAKE, 1, 2, 40000, 0.0, 50, 1, FAKE, 32768, step, FAKE, FAKE, None) == I
+    # workspace sizes: n rows of v logits, -1 outside the limits
+    ws = lib.moat_sample_workspace_size(2, 1000)
+    sws = lib.moat_lut_softmax_workspace_size(2, 1000)
+    assert 2 * 2 * 1000 < ws and 0 < sws < ws
+    assert lib.moat_sample_workspace_size(0, 1000) == 0 and lib.moat_lut_softmax_workspace_size(0, 5) == 0
+    assert lib.moat_sample_workspace_size(2, 0) == -1 and lib.moat_sample_workspace_size(-1, 10) == -1
+    assert lib.moat_sample_workspace_size(1, 524288) > 2 * 524288
+    assert lib.moat_sample_workspace_size(1, 524289) == -1 and lib.moat_lut_softmax_workspace_size(1, 524289) == -1
+    assert lib.moat_sample_workspace_size((1 << 22) + 1, 10) == -1
+    big = lib.moat_sample_workspace_size(1 << 22, 1 << 19)  # 64-bit byte counts
+    assert big > 2 * (1 << 22) * (1 << 19)
+
+    # moat_lut_softmax(x, dtype, n, v, lut, lut_size, step, probs, workspace, bytes, stream)
+    def sm(x, dtype, n, v, lut_size, st, probs, w=FAKE, nbytes=sws):
+        return lib.moat_lut_softmax(x, dtype, n, v, FAKE, lut_size, st, probs, w, nbytes, None)
+    assert sm(FAKE, 0, 2, 1000, 32768, step, None) == I  # no output
+    assert sm(FAKE, 2, 2, 1000, 32768, step, FAKE) == I  # int8 logits
+    assert sm(FAKE, 0, 2, 524289, 32768, step, FAKE) == I  # row above 64 chunks of 8192
+    assert sm(FAKE, 0, 2, 0, 32768, step, FAKE) == I
+    assert sm(FAKE, 0, 2, 1000, (1 << 24) + 1, step, FAKE) == I  # table index past float32's integers
+    assert sm(FAKE, 0, 2, 1000, 1, step, FAKE) == I
+    assert sm(FAKE, 0, 2, 1000, 32768, F(0.0), FAKE) == I
+    assert sm(FAKE, 0, 2, 1000, 32768, F(float("inf")), FAKE) == I
+    assert sm(ctypes.c_void_p(0x10002), 0, 2, 1000, 32768, step, FAKE) == I
+    assert sm(ctypes.c_void_p(0x10004), 3, 2, 1000, 32768, step, FAKE) == I  # f64: 8 B
+    assert sm(FAKE, 0, 2, 1000, 32768, step, FAKE, w=None) == W
+    assert sm(FAKE, 0, 2, 1000, 32768, step, FAKE, nbytes=sws - 1) == W
+    assert sm(FAKE, 0, 2, 1000, 32768, step, FAKE, w=ctypes.c_void_p(0x10080)) == W  # 256-byte alignment
+    assert sm(FAKE, 0, 0, 1000, 32768, step, None, w=None, nbytes=0) == _lib.MOAT_OK  # no rows
+
+    # moat_sample_tokens(x, dtype, n, v, T, top_k, seed, lut, lut_size, step, tokens, logprobs, workspace,
+    #                    bytes, stream)
+    def st(dtype, n, v, t, k, tok=FAKE, lp=FAKE, w=FAKE, nbytes=ws):
+        return lib.moat_sample_tokens(FAKE, dtype, n, v, t, k, 1, FAKE, 32768, step, tok, lp, w, nbytes, None)
+    assert st(0, 2, 1000, 0.7, 0) == I
+    assert st(0, 2, 1000, 0.7, 65) == I
+    assert st(0, 2, 1000, float("nan"), 50) == I
+    assert st(0, 2, 1000, 0.7, 50, tok=None) == I
+    assert st(0, 2, 1000, 0.7, 50, lp=ctypes.c_void_p(0x10002)) == I
+    assert st(1, 2, 600000, 0.0, 50) == I
+    assert st(0, 2, 1000, 0.7, 50, nbytes=sws) == W  # the softmax's size lacks the table values
+    assert st(0, 2, 1000, 0.0, 50, w=None) == W
     assert lib.moat_lut_lookup(FAKE, -1, FAKE, 32768, step, FAKE, None) == I
     assert lib.moat_lut_lookup(FAKE, 4, FAKE, 1, step, FAKE, None) == I
     assert lib.moat_lut_lookup(ctypes.c_void_p(0x10002), 4, FAKE, 32768, step, FAKE, None) == I
@@ -216,7 +238,7 @@ def test_sampling_python_checks_first():
     with pytest.raises(ValueError):
         sampling.TokenSampler(top_k=65)
     with pytest.raises(ValueError):
-        sampling.TokenSampler(exp_lut_size=40000)
+        sampling.TokenSampler(exp_lut_size=(1 << 24) + 1)
     lut = sampling.ExponentialLUT()
     assert lut.memory_bytes == 65536 and lut.lut.dtype == np.float16 and lut.size == 32768
 

@@ -26,10 +26,16 @@ def _rows(n, v, seed, dtype=np.float32, scale=3.0):
         x[2, ::3] = -np.inf  # -inf logits are exp(-10) entries
     if n > 3:
         x[3] = 0.5  # uniform row: all ties
+    if n > 4 and v > 2:
+        # 60 equal maxima spread over the row (across its 8192-logit chunks
+        # when it has several): the top 50 are the 50 lowest indices among them
+        x[4, np.unique(np.linspace(v - 1, 0, 60).astype(np.int64))] = np.abs(x[4]).max() + 1.0
     return x.astype(dtype)
 
 
 VOCABS = [1, 2, 7, 8, 9, 50, 100, 128, 129, 136, 540, 1000, 4096, 8192, 8193, 16385, 32000, 32768]
+# GPT-2, Llama-3 and Qwen-2.5 vocabularies and the largest row (64 chunks)
+LARGE_VOCABS = [50257, 128256, 151936, 524288]
 
 
 def test_lookup_matches_oracle():
@@ -80,7 +86,32 @@ def test_softmax_axes_and_small_tables():
     with pytest.raises(ValueError):
         safe_softmax_lut(np.zeros((2, 0), np.float32), lut)
     with pytest.raises(ValueError):
-        safe_softmax_lut(np.zeros((1, 32769), np.float32), lut)
+        safe_softmax_lut(np.zeros((1, 524289), np.float32), lut)
+
+
+def test_large_vocabularies():
+    """Rows of many chunks: softmax (float32), greedy (fp16) and sampling
+    (float32 at T = 0.7, float64 at T = 3) bit for bit against the oracle."""
+    from moat_amd.sampling import ExponentialLUT, TokenSampler, safe_softmax_lut
+    lut, sampler = ExponentialLUT(), TokenSampler()
+    table, step = S.exp_table(), S.table_step_f32()
+    for v in LARGE_VOCABS:
+        say(f"case: large v={v} softmax")
+        x = _rows(5, v, 700 + v)
+        got = safe_softmax_lut(x, lut)
+        assert np.array_equal(got.view(np.uint16), S.softmax_lut(x, table, step).view(np.uint16)), v
+        say(f"case: large v={v} greedy")
+        x = _rows(6, v, 800 + v, np.float16)
+        tok, lp = sampler.sample_tokens(x, temperature=0.0)
+        wt, wl = S.sample_tokens(x, temperature=0.0)
+        assert np.array_equal(tok, wt) and np.array_equal(lp.view(np.uint16), wl.view(np.uint16)), (v, tok, wt)
+        for dtype, temp in ((np.float32, 0.7), (np.float64, 3.0)):
+            say(f"case: large v={v} sample dtype={np.dtype(dtype).name} T={temp}")
+            x = _rows(7, v, 900 + v, dtype)
+            tok, lp = sampler.sample_tokens(x, temperature=temp, seed=99 + v)
+            wt, wl = S.sample_tokens(x, temperature=temp, seed=99 + v)
+            assert np.array_equal(tok, wt), (v, temp, tok, wt)
+            assert np.array_equal(lp.view(np.uint32), wl.view(np.uint32)), (v, temp, lp, wl)
 
 
 @pytest.mark.parametrize("dtype", [np.float32, np.float16, np.float64])
@@ -195,6 +226,24 @@ def test_non_finite_rows():
         assert list(tok[:3]) == [30, 7, 0] and np.all(np.isnan(lp[:3].astype(np.float32)))
         wt, wl = S.sample_tokens(x, temperature=temp, seed=1)
         assert np.array_equal(tok, wt) and np.array_equal(lp, wl, equal_nan=True)
+    # the same over a row of three 8192-logit chunks: the first NaN, the
+    # first +inf and the first of equal maxima in different chunks
+    say("case: non-finite rows, three chunks")
+    x = np.random.default_rng(3).standard_normal((4, 20000)).astype(np.float32)
+    x[0, 17000], x[0, 9000] = np.nan, np.nan
+    x[1, 19999], x[1, 12000] = np.inf, np.inf
+    x[2, 300], x[2, 8200], x[2, 16500] = 49.0, 50.0, 50.0
+    p = safe_softmax_lut(x, ExponentialLUT())
+    assert np.all(np.isnan(p[:2].astype(np.float32)))
+    want = S.softmax_lut(x[2:], S.exp_table(), S.table_step_f32())
+    assert np.array_equal(p[2:].view(np.uint16), want.view(np.uint16))
+    for temp in (0.0, 0.7):
+        tok, lp = sampler.sample_tokens(x, temperature=temp, seed=5)
+        assert list(tok[:2]) == [9000, 12000] and np.all(np.isnan(lp[:2].astype(np.float32)))
+        if temp == 0.0:
+            assert tok[2] == 8200
+        wt, wl = S.sample_tokens(x, temperature=temp, seed=5)
+        assert np.array_equal(tok, wt) and np.array_equal(lp, wl, equal_nan=True)
 
 
 def test_lm_head_logits_sampled_on_the_gpu():
@@ -218,3 +267,23 @@ def test_lm_head_logits_sampled_on_the_gpu():
         assert np.array_equal(tok.cpu().numpy(), wt)
         assert np.array_equal(lp.cpu().numpy().view(np.uint16 if temp == 0 else np.uint32),
                               wl.view(np.uint16 if temp == 0 else np.uint32))
+
+
+def test_workspace_counters_return_to_zero():
+    """The per-row counters at the start of the sampling workspace (the last
+    of a row's chunk workgroups takes over the row) are zero after every
+    call, so one workspace serves calls of any shape in turn."""
+    import torch
+    from moat_amd import _device as D
+    from moat_amd.sampling import TokenSampler
+    say("case: workspace counters")
+    sampler = TokenSampler()
+    x = _rows(9, 20000, 31)  # three chunks per row
+    for temp in (0.0, 0.7, 0.0, 2.0):
+        tok, lp = sampler.sample_tokens(x, temperature=temp, seed=8)
+        wt, wl = S.sample_tokens(x, temperature=temp, seed=8)
+        assert np.array_equal(tok, wt) and np.array_equal(lp.view(np.uint16 if temp == 0 else np.uint32),
+                                                          wl.view(np.uint16 if temp == 0 else np.uint32))
+        torch.cuda.synchronize()
+        ws = D.sample_workspaces.get(1)
+        assert int(torch.count_nonzero(ws[:4 * 9])) == 0, temp
