@@ -153,6 +153,9 @@ def main() -> int:
     ap.add_argument("--finish", type=int, default=0, help="split-K hand-off (0 auto, 1 atomics, 2 fences, 3 kernel)")
     ap.add_argument("--front", type=int, default=0,
                     help="load front end (0 auto, 1 LDS-staged, 2 direct, 3 LDS DMA, 4 record stream)")
+    ap.add_argument("--tile-order", action="store_true",
+                    help="GEMM configs: weights stored in tile order (each 256-column tile's rows contiguous; "
+                         "moat_int4_records_to_tiles), read by moat_int4_gemm_tiles; needs M % 256 == 0")
     ap.add_argument("--fused", action="store_true",
                     help="layer_h2048: Q, K, V in one launch and gate/up fused with SwiGLU (h feeds down)")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"), default=None,
@@ -185,12 +188,15 @@ def main() -> int:
 
     import torch
     from moat_amd import _lib
-    from moat_amd.dequant import _gemm_into, quantize_to_superblocks
+    from moat_amd.dequant import _gemm_into, quantize_to_superblocks, records_to_tiles
 
     lib = _lib.load()
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     K, M, std, seed, outl, default_ns = CONFIGS[args.config]
+    if args.tile_order and M % 256 != 0:
+        print(f"--tile-order needs M % 256 == 0 (M = {M})", file=sys.stderr)
+        return 2
     ns = [int(v) for v in args.ns.split(",")] if args.ns else default_ns
 
     rng = np.random.default_rng(seed)
@@ -202,6 +208,8 @@ def main() -> int:
         w.reshape(-1)[pos] = rng.choice(np.array([-1.0, 1.0], np.float32), size=n_out) * np.float32(8 * std)
     blob0 = quantize_to_superblocks(torch.from_numpy(w).to(dev))  # (S, 144) uint8 on the GPU
     del w
+    if args.tile_order:
+        blob0 = records_to_tiles(blob0, K, M)
     sb_bytes = blob0.numel()
     copies = max(2, -(-ROTATE_BYTES // sb_bytes))
     blobs = [blob0] + [blob0.clone() for _ in range(copies - 1)]
@@ -213,7 +221,7 @@ def main() -> int:
 
     def one_call(N, i):
         _gemm_into(xs[N], blobs[i % copies], ys[N], K, M, args.algo, args.splits, args.batch, args.finish,
-                   args.front)
+                   args.front, tile_order=args.tile_order)
 
     # All timed work is replayed from HIP graphs captured on one stream, so the
     # timed region holds back-to-back kernels and no Python launch overhead.
@@ -321,7 +329,8 @@ def main() -> int:
         "config": {"workload": WORKLOAD_NAMES[args.config], "K": K, "M": M, "ns": ns,
                    "weight_copies_rotated": copies, "timing": "HIP graph replay, HIP events on the launch stream",
                    "algo": args.algo, "splits": args.splits, "batch": args.batch, "finish": args.finish,
-                   "front": args.front, "weights": "int4 superblocks (144 B per 256 weights)",
+                   "front": args.front, "weights": "int4 superblocks (144 B per 256 weights)"
+                   + (", tile order" if args.tile_order else ", row order"),
                    "activations": "fp16", "output": "fp32"},
         "per_n": {str(k): v for k, v in per_n.items()},
         "roofline": roof,

@@ -138,6 +138,29 @@ int32_t moat_int4_gemm_ex(const uint16_t* x_f16, const uint8_t* superblocks, flo
                           int32_t n, int32_t k, int32_t m, const moat_int4_gemm_options* options,
                           void* workspace, int64_t workspace_bytes, hipStream_t stream);
 
+/*
+ * Tile order: the same 144-byte records of W[K][M] (M % 256 == 0), stored so
+ * that each 256-column tile's K rows of records are contiguous (row r of tile
+ * j at record j*K + r) instead of row by row (record r*(M/256) + j).  In the
+ * row order a tile's rows lie 144*M/256 bytes apart, and a load-only kernel
+ * reads that pattern at about 4 TB/s on MI355X; in tile order each 32-row
+ * round of a tile is one 4608-byte block and reads like a plain stream
+ * (about 5.6 TB/s).  No counterpart in the reference, whose stream is the row
+ * order (src/dequant.py:116-147): a storage order a loader chooses once.
+ *
+ * moat_int4_records_to_tiles: copies a row-order stream to tile order
+ * (k >= 1, m % 256 == 0; both 16-byte aligned, not overlapping).
+ * moat_int4_gemm_tiles: moat_int4_gemm_ex over a tile-order stream, with the
+ * same plan, kernel and result bits; it needs the record-stream kernel
+ * (m % 256 == 0, k % 32 == 0, x 16-byte aligned; MOAT_ERR_INVALID
+ * otherwise).  Workspace from moat_int4_gemm_ex_workspace_size.
+ */
+int32_t moat_int4_records_to_tiles(const uint8_t* superblocks, int32_t k, int32_t m, uint8_t* tiles,
+                                   hipStream_t stream);
+int32_t moat_int4_gemm_tiles(const uint16_t* x_f16, const uint8_t* tiles, float* y_f32,
+                             int32_t n, int32_t k, int32_t m, const moat_int4_gemm_options* options,
+                             void* workspace, int64_t workspace_bytes, hipStream_t stream);
+
 /* Zero `bytes` bytes of device memory with a kernel (no memset node). */
 int32_t moat_int4_workspace_clear(void* workspace, int64_t bytes, hipStream_t stream);
 

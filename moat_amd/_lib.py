@@ -47,6 +47,8 @@ SIGNATURES = {
     "moat_int4_gemm": (_I32, [_P, _P, _P, _I32, _I32, _I32, _P, _I64, _P]),
     "moat_int4_gemm_ex_workspace_size": (_I64, [_I32, _I32, _I32, ctypes.POINTER(GemmOptions)]),
     "moat_int4_gemm_ex": (_I32, [_P, _P, _P, _I32, _I32, _I32, ctypes.POINTER(GemmOptions), _P, _I64, _P]),
+    "moat_int4_records_to_tiles": (_I32, [_P, _I32, _I32, _P, _P]),
+    "moat_int4_gemm_tiles": (_I32, [_P, _P, _P, _I32, _I32, _I32, ctypes.POINTER(GemmOptions), _P, _I64, _P]),
     "moat_int4_workspace_clear": (_I32, [_P, _I64, _P]),
     "moat_int4_gemm_multi_workspace_size": (_I64, [_I32, _I32, _I32, _I32]),
     "moat_int4_gemm_multi": (_I32, [_P, _P, _P, _I32, _I32, _I32, _I32, _P, _I64, _P]),

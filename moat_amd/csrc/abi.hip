@@ -42,7 +42,8 @@ hipError_t launch_lut_lookup(const float* x, int64_t n, const uint16_t* lut, int
                              hipStream_t st);
 hipError_t launch_gemm(int algo, const uint16_t* x, const uint8_t* sb, float* y, int n, int k, int m, int splits,
                        int batch, int finish, int front, int group, int waves, float* partials,
-                       uint32_t* counters, hipStream_t stream);
+                       uint32_t* counters, int tile_order, hipStream_t stream);
+hipError_t launch_records_to_tiles(const uint8_t* sb, int k, int m, uint8_t* tiles, hipStream_t stream);
 }  // namespace moat
 
 namespace {
@@ -292,6 +293,31 @@ bool sample_ws_ok(int32_t n, int32_t v, bool with_e, const void* workspace, int6
 }
 
 
+// The GEMM over records in row order (tile_order 0) or tile order (1).
+int32_t gemm_call(const uint16_t* x_f16, const uint8_t* superblocks, float* y_f32, int32_t n, int32_t k, int32_t m,
+                  const moat_int4_gemm_options* options, void* workspace, int64_t workspace_bytes, int tile_order,
+                  hipStream_t stream) {
+  if (!gemm_shape_ok(n, k, m) || !options_ok(options, n)) return MOAT_ERR_INVALID;
+  if (!x_f16 || !superblocks || !y_f32) return MOAT_ERR_INVALID;
+  if (!aligned(x_f16, 2) || !aligned(superblocks, 16) || !aligned(y_f32, 4)) return MOAT_ERR_INVALID;
+  const GemmPlan p = plan_gemm(n, k, m, options);
+  if (p.algo == MOAT_GEMM_DOT2 && n > kMaxDot2N) return MOAT_ERR_INVALID;
+  // tile order: the record-stream kernel only (whole 256-column tiles, whole
+  // 32-row rounds, 16-byte X rows)
+  if (tile_order && (p.front != 3 || (m % 256) != 0 || (k % 32) != 0 || !aligned(x_f16, 16) || (k % 8) != 0))
+    return MOAT_ERR_INVALID;
+  float* partials = nullptr;
+  uint32_t* counters = nullptr;
+  if (p.workspace_bytes > 0) {
+    if (!workspace || workspace_bytes < p.workspace_bytes || !aligned(workspace, 16)) return MOAT_ERR_WORKSPACE;
+    counters = static_cast<uint32_t*>(workspace);
+    partials = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + p.counter_bytes);
+  }
+  return status_of(moat::launch_gemm(p.algo, x_f16, superblocks, y_f32, n, k, m, p.splits, p.batch, p.finish,
+                                     p.front, p.group, p.waves, partials, counters, tile_order, stream));
+}
+
+
 int sample_dtype(int32_t dtype) { return dtype == MOAT_DTYPE_F32 ? 0 : dtype == MOAT_DTYPE_F16 ? 1 : 2; }
 
 }  // namespace
@@ -329,20 +355,24 @@ int64_t moat_int4_gemm_workspace_size(int32_t n, int32_t k, int32_t m) {
 int32_t moat_int4_gemm_ex(const uint16_t* x_f16, const uint8_t* superblocks, float* y_f32, int32_t n, int32_t k,
                           int32_t m, const moat_int4_gemm_options* options, void* workspace, int64_t workspace_bytes,
                           hipStream_t stream) {
-  if (!gemm_shape_ok(n, k, m) || !options_ok(options, n)) return MOAT_ERR_INVALID;
-  if (!x_f16 || !superblocks || !y_f32) return MOAT_ERR_INVALID;
-  if (!aligned(x_f16, 2) || !aligned(superblocks, 16) || !aligned(y_f32, 4)) return MOAT_ERR_INVALID;
-  const GemmPlan p = plan_gemm(n, k, m, options);
-  if (p.algo == MOAT_GEMM_DOT2 && n > kMaxDot2N) return MOAT_ERR_INVALID;
-  float* partials = nullptr;
-  uint32_t* counters = nullptr;
-  if (p.workspace_bytes > 0) {
-    if (!workspace || workspace_bytes < p.workspace_bytes || !aligned(workspace, 16)) return MOAT_ERR_WORKSPACE;
-    counters = static_cast<uint32_t*>(workspace);
-    partials = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + p.counter_bytes);
-  }
-  return status_of(moat::launch_gemm(p.algo, x_f16, superblocks, y_f32, n, k, m, p.splits, p.batch, p.finish,
-                                     p.front, p.group, p.waves, partials, counters, stream));
+  return gemm_call(x_f16, superblocks, y_f32, n, k, m, options, workspace, workspace_bytes, 0, stream);
+}
+
+int32_t moat_int4_gemm_tiles(const uint16_t* x_f16, const uint8_t* tiles, float* y_f32, int32_t n, int32_t k,
+                             int32_t m, const moat_int4_gemm_options* options, void* workspace,
+                             int64_t workspace_bytes, hipStream_t stream) {
+  return gemm_call(x_f16, tiles, y_f32, n, k, m, options, workspace, workspace_bytes, 1, stream);
+}
+
+int32_t moat_int4_records_to_tiles(const uint8_t* superblocks, int32_t k, int32_t m, uint8_t* tiles,
+                                   hipStream_t stream) {
+  if (k < 1 || m < 256 || (m % 256) != 0) return MOAT_ERR_INVALID;
+  if ((int64_t)k * (m / 256) > ((int64_t)1 << 40)) return MOAT_ERR_INVALID;
+  if (!superblocks || !tiles || !aligned(superblocks, 16) || !aligned(tiles, 16)) return MOAT_ERR_INVALID;
+  const int64_t bytes = (int64_t)k * (m / 256) * 144;
+  const uintptr_t a = reinterpret_cast<uintptr_t>(superblocks), b = reinterpret_cast<uintptr_t>(tiles);
+  if (a < b + (uintptr_t)bytes && b < a + (uintptr_t)bytes) return MOAT_ERR_INVALID;  // the copies overlap
+  return status_of(moat::launch_records_to_tiles(superblocks, k, m, tiles, stream));
 }
 
 int32_t moat_int4_gemm(const uint16_t* x_f16, const uint8_t* superblocks, float* y_f32, int32_t n, int32_t k,

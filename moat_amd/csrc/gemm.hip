@@ -96,6 +96,15 @@ struct GemmParams {
   int y_vec;               // y and the partials are 16-byte aligned and m % 4 == 0: float4 stores
   int items_base;          // records kernel (stream-K): workgroup p covers items (tile * rounds + round)
   int items_rem;           //   [p*base + min(p, rem), +base + (p < rem))
+  // Records kernel: where a tile's records lie.  Row order (the stream as
+  // written): round stride 32 rows of M/256 records (18 * M bytes), tile
+  // stride one record (144 bytes), rows M/256 records apart (rec_row_m = M).
+  // Tile order (each 256-column tile's K rows of records contiguous, tiles
+  // in column order): round stride 32 records (4608 bytes), tile stride K
+  // records, rows one record apart (rec_row_m = 256).
+  uint64_t rec_round_bytes;
+  uint64_t rec_tile_bytes;
+  int rec_row_m;
   // Record-stream kernel over several matrices of one shape that share X:
   // kModeMulti: tile t of the concatenated tile space is tile t - i*tiles of
   // matrix i = t / tiles (Y_i = X @ W_i); kModeSwiglu: tile group g pairs tile
@@ -1121,9 +1130,9 @@ __global__ void __launch_bounds__(kW * 64) int4_gemm_records_kernel(GemmParams P
   int lo, hi;
   streamk_range(P, p, lo, hi);
 
-  const uint64_t round_bytes = (uint64_t)18 * (uint64_t)P.m;
+  const uint64_t round_bytes = P.rec_round_bytes;
   RecSlots slots;
-  rec_slots(slots, lane, P.m);
+  rec_slots(slots, lane, P.rec_row_m);
   uint8_t* ring = smem + wave * kDepth * G::kStageBytes;
   const uint32_t ring_lds = (uint32_t)(uintptr_t)(lds_ptr_t)ring;  // LDS byte address (wave-uniform)
   float* red = reinterpret_cast<float*>(smem);
@@ -1154,7 +1163,7 @@ __global__ void __launch_bounds__(kW * 64) int4_gemm_records_kernel(GemmParams P
 #pragma unroll
     for (int i = 0; i < kRecWeightLoads; ++i) woff[i] = groups < 8 ? slots.half[i] : slots.full[i];
     const uint8_t* wmat = kMode == kModeSingle ? P.sb : select4(mat, P.sbm[0], P.sbm[1], P.sbm[2], P.sbm[3]);
-    const uint8_t* wtile = wmat + (uint64_t)kSbBytes * (has_tile ? ltile : 0);
+    const uint8_t* wtile = wmat + P.rec_tile_bytes * (uint64_t)(has_tile ? ltile : 0);
     // where the group's results go (the group's first tile)
     RecOut out;
     if (kMode == kModeSingle) {
@@ -1456,7 +1465,7 @@ bool gemm_fused_shares_tiles(int mode, int mats, int k, int m, int wgs) {
 
 hipError_t launch_gemm(int algo, const uint16_t* x, const uint8_t* sb, float* y, int n, int k, int m, int splits,
                        int batch, int finish, int front, int group, int waves, float* partials, uint32_t* counters,
-                       hipStream_t stream) {
+                       int tile_order, hipStream_t stream) {
   GemmParams P = {};
   P.x = x; P.sb = sb; P.y = y; P.partials = partials; P.counters = counters;
   P.n = n; P.k = k; P.m = m; P.splits = splits; P.rounds = gemm_rounds(k); P.tiles = gemm_col_tiles(m);
@@ -1480,6 +1489,15 @@ hipError_t launch_gemm(int algo, const uint16_t* x, const uint8_t* sb, float* y,
       P.items_base = items / wgs;
       P.items_rem = items % wgs;
       P.y_vec = ((reinterpret_cast<uintptr_t>(y) & 15) == 0) ? 1 : 0;
+      if (tile_order) {  // the caller has checked M % 256 == 0
+        P.rec_round_bytes = (uint64_t)kRoundRows * kSbBytes;
+        P.rec_tile_bytes = (uint64_t)k * kSbBytes;
+        P.rec_row_m = kRecCols;
+      } else {
+        P.rec_round_bytes = (uint64_t)18 * (uint64_t)m;
+        P.rec_tile_bytes = kSbBytes;
+        P.rec_row_m = m;
+      }
       e = P.n <= 16 ? launch_records<1>(P, wgs, batch, group_tiles, waves, stream)
                     : launch_records<2>(P, wgs, batch, group_tiles, waves, stream);
       if (e != hipSuccess || !gemm_records_shares_tiles(k, m, group_tiles, wgs) || finish != kFinishSecondKernel)
@@ -1490,6 +1508,7 @@ hipError_t launch_gemm(int algo, const uint16_t* x, const uint8_t* sb, float* y,
       hipLaunchKernelGGL(streamk_fixup_kernel, dim3(blocks), dim3(256), 0, stream, P, group_tiles, (int)kModeSingle);
       return hipGetLastError();
     }
+    if (tile_order) return hipErrorInvalidValue;  // the tile order has only the records kernel
     front = kFrontVgprLds;
   }
   // the staged front ends need M % 64 == 0 (4-byte aligned scale pairs)
@@ -1523,6 +1542,9 @@ hipError_t launch_gemm_fused(int mode, const uint16_t* x, const uint8_t* const* 
   P.items_base = items / wgs;
   P.items_rem = items % wgs;
   P.mats = mats;
+  P.rec_round_bytes = (uint64_t)18 * (uint64_t)m;
+  P.rec_tile_bytes = kSbBytes;
+  P.rec_row_m = m;
   int y_vec = 1;
   for (int i = 0; i < 4; ++i) {
     P.sbm[i] = sbs[i < mats ? i : 0];
@@ -1544,6 +1566,28 @@ hipError_t launch_gemm_fused(int mode, const uint16_t* x, const uint8_t* const* 
   int blocks = (quads + 255) / 256;
   if (blocks > 2048) blocks = 2048;
   hipLaunchKernelGGL(streamk_fixup_kernel, dim3(blocks), dim3(256), 0, stream, P, mode == kModeSwiglu ? 2 : 1, mode);
+  return hipGetLastError();
+}
+
+// Records of W[K][M] (M % 256 == 0) from row order to tile order: record
+// (row r, tile j) moves from r * (M/256) + j to j * K + r.  One thread per
+// 16-byte chunk (9 per record), reading the source in order.
+__global__ void records_to_tiles_kernel(const uint4* __restrict__ src, int64_t k, int64_t tiles, uint4* __restrict__ dst) {
+  const int64_t chunks = k * tiles * 9;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < chunks; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t rec = i / 9, c = i - rec * 9;
+    const int64_t r = rec / tiles, j = rec - r * tiles;
+    dst[(j * k + r) * 9 + c] = src[i];
+  }
+}
+
+hipError_t launch_records_to_tiles(const uint8_t* sb, int k, int m, uint8_t* tiles, hipStream_t stream) {
+  const int64_t chunks = (int64_t)k * (m / kRecCols) * 9;
+  if (chunks == 0) return hipSuccess;
+  int64_t blocks = (chunks + 255) / 256;
+  if (blocks > 8192) blocks = 8192;
+  hipLaunchKernelGGL(records_to_tiles_kernel, dim3((unsigned)blocks), dim3(256), 0, stream,
+                     reinterpret_cast<const uint4*>(sb), (int64_t)k, (int64_t)(m / kRecCols), reinterpret_cast<uint4*>(tiles));
   return hipGetLastError();
 }
 

@@ -280,7 +280,7 @@ def quantize_to_superblocks(weights, scale_rule: str = "f32"):
 
 def _gemm_into(x: torch.Tensor, blob: torch.Tensor, y: torch.Tensor, K: int, M: int,
                algo: int = _lib.GEMM_AUTO, splits: int = 0, batch: int = 0, finish: int = 0, front: int = 0,
-               group: int = 0, waves: int = 0) -> None:
+               group: int = 0, waves: int = 0, tile_order: bool = False) -> None:
     lib = _lib.load()
     n = x.shape[0]
     opt = _lib.GemmOptions(algo, splits, batch, finish, front, group, waves)
@@ -289,8 +289,27 @@ def _gemm_into(x: torch.Tensor, blob: torch.Tensor, y: torch.Tensor, K: int, M: 
         raise ValueError(f"unsupported GEMM configuration N={n} K={K} M={M} algo={algo} splits={splits} "
                          f"batch={batch} finish={finish} front={front} group={group} waves={waves}")
     ws = D.workspaces.get(ws_bytes)
-    _lib.check(lib.moat_int4_gemm_ex(D.ptr(x), D.ptr(blob), D.ptr(y), n, K, M, ctypes.byref(opt),
-                                     D.ptr(ws), ws_bytes, D.stream()), "batched_int4_matmul")
+    fn = lib.moat_int4_gemm_tiles if tile_order else lib.moat_int4_gemm_ex
+    _lib.check(fn(D.ptr(x), D.ptr(blob), D.ptr(y), n, K, M, ctypes.byref(opt), D.ptr(ws), ws_bytes, D.stream()),
+               "batched_int4_matmul")
+
+
+def records_to_tiles(superblocks, K: int, M: int) -> torch.Tensor:
+    """The 144-byte records of a row-major K x M stream (``M % 256 == 0``) in
+    tile order: the K rows of each 256-column tile contiguous, tiles in
+    column order (row r of tile j at record ``j * K + r``).  A GPU uint8
+    tensor; :func:`batched_int4_matmul` reads it with ``tile_order=True``,
+    with the same result bits and a faster weight stream.  (A storage order
+    of this build; the reference's stream is the row order.)"""
+    K, M = int(K), int(M)
+    if K < 1 or M < 256 or M % 256 != 0:
+        raise ValueError(f"tile order needs M % 256 == 0 (got K={K}, M={M})")
+    n_sb = K * M // SUPERBLOCK_ELEMS
+    blob = _blob_to_device(superblocks, n_sb)
+    tiles = torch.empty(n_sb * SUPERBLOCK_BYTES, dtype=torch.uint8, device=blob.device)
+    _lib.check(_lib.load().moat_int4_records_to_tiles(D.ptr(blob), K, M, D.ptr(tiles), D.stream()),
+               "records_to_tiles")
+    return tiles
 
 
 def _fused_inputs(x, K: int, M: int, blobs):
@@ -377,14 +396,16 @@ def _swiglu_into(x: torch.Tensor, gate: torch.Tensor, up: torch.Tensor, h: torch
 
 def batched_int4_matmul(x, superblocks, K: int, M: int, out=None, *, algo: int = _lib.GEMM_AUTO,
                         splits: int = 0, batch: int = 0, finish: int = 0, front: int = 0, group: int = 0,
-                        waves: int = 0):
+                        waves: int = 0, tile_order: bool = False):
     """``Y[N, M] = f32(X[N, K]) @ f32(deq(W)[K, M])`` with W the 144-byte stream
     of a row-major K x M matrix; fp32 out.  Equal (to float32 summation order)
     to decoding with :func:`unpack_superblock_weights` and a float32 matmul.
     ValueError unless ``M % 32 == 0`` and ``K*M % 256 == 0``.  N above 32 is
     processed in slices of 32 rows.  ``algo``/``splits``/``batch``/``finish``/
     ``front``/``group``/``waves`` override the launch choices of
-    ``moat_int4_gemm_options`` (0 = automatic)."""
+    ``moat_int4_gemm_options`` (0 = automatic).  ``tile_order``: the stream is
+    in the tile order of :func:`records_to_tiles` (``M % 256 == 0``,
+    ``K % 32 == 0``)."""
     want_t = D.is_tensor(x)
     K, M = int(K), int(M)
     if K < 1 or M < 32 or M % 32 != 0 or (K * M) % SUPERBLOCK_ELEMS != 0:
@@ -408,7 +429,7 @@ def batched_int4_matmul(x, superblocks, K: int, M: int, out=None, *, algo: int =
         y = torch.empty((N, M), dtype=torch.float32, device=xs.device)
     for r0 in range(0, N, MAX_BATCH_PER_CALL):
         r1 = min(N, r0 + MAX_BATCH_PER_CALL)
-        _gemm_into(xs[r0:r1], blob, y[r0:r1], K, M, algo, splits, batch, finish, front, group, waves)
+        _gemm_into(xs[r0:r1], blob, y[r0:r1], K, M, algo, splits, batch, finish, front, group, waves, tile_order)
     if out is not None and not D.is_tensor(out):
         np.copyto(out, D.to_host(y))
         return out

@@ -28,6 +28,8 @@ How each function is pinned (tests/test_oracle.py):
   tie-constructed groups, and the reference tests' known answers;
 * packing: the reference kernel test's byte 0x7F answer, the reference
   runner's 0x77 stream, round trips and Python-int bit arithmetic;
+* tile order: a Python-loop index permutation on small shapes, and every
+  tile's records decoding to that tile's 256 columns of W;
 * GEMM: float64 accumulation of the same products, the closed-form
   -0.5*K answer of the reference runner's synthetic stream, and
   row-by-row GEMV equality.
@@ -254,6 +256,16 @@ def decode_superblocks(blob, num_superblocks: int) -> np.ndarray:
     with np.errstate(over="ignore", invalid="ignore"):
         out = (vals * scales[:, :, None]).astype(np.float16)
     return out.reshape(-1)
+
+
+def records_to_tiles(blob, K: int, M: int) -> np.ndarray:
+    """The records of a row-major K x M stream (M % 256 == 0) in tile order:
+    record (row r, 256-column tile j) moves from ``r * (M/256) + j`` to
+    ``j * K + r`` (a storage order of this build, no reference counterpart:
+    the records themselves are unchanged)."""
+    t = M // SB_ELEMS
+    rec = np.asarray(blob, dtype=np.uint8).reshape(K, t, SB_BYTES)
+    return np.ascontiguousarray(rec.transpose(1, 0, 2)).reshape(-1)
 
 
 # --------------------------------------------------------------------------

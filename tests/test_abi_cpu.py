@@ -262,3 +262,31 @@ def test_product_refuses_to_run_without_gpu():
     from moat_amd import dequant
     with pytest.raises(RuntimeError, match="GPU"):
         dequant.unpack_superblock_weights(np.zeros(144, dtype=np.uint8), 1)
+
+
+def test_tile_order_entry_points_validate(lib):
+    I = _lib.MOAT_ERR_INVALID
+    opt = _lib.GemmOptions(0, 0, 0, 0, 0, 0, 0)
+    # moat_int4_records_to_tiles(sb, k, m, tiles, stream)
+    assert lib.moat_int4_records_to_tiles(FAKE, 64, 384, ctypes.c_void_p(0x90000000), None) == I  # m % 256
+    assert lib.moat_int4_records_to_tiles(FAKE, 0, 512, ctypes.c_void_p(0x90000000), None) == I
+    assert lib.moat_int4_records_to_tiles(FAKE, 64, 512, FAKE, None) == I  # overlapping copies
+    assert lib.moat_int4_records_to_tiles(ctypes.c_void_p(0x10008), 64, 512, ctypes.c_void_p(0x90000000),
+                                          None) == I  # 16-byte alignment
+    assert lib.moat_int4_records_to_tiles(None, 64, 512, ctypes.c_void_p(0x90000000), None) == I
+    # moat_int4_gemm_tiles(x, tiles, y, n, k, m, options, workspace, bytes, stream): the record-stream kernel only
+    big = ctypes.c_void_p(0x90000000)
+    assert lib.moat_int4_gemm_tiles(FAKE, FAKE, big, 1, 2048, 5504, ctypes.byref(opt), big, 1 << 30, None) == I
+    assert lib.moat_int4_gemm_tiles(FAKE, FAKE, big, 1, 48, 512, ctypes.byref(opt), big, 1 << 30, None) == I
+    assert lib.moat_int4_gemm_tiles(ctypes.c_void_p(0x10008), FAKE, big, 1, 2048, 2048, ctypes.byref(opt), big,
+                                    1 << 30, None) == I  # X rows need 16-byte loads
+    dot2 = _lib.GemmOptions(_lib.GEMM_DOT2, 0, 0, 0, 0, 0, 0)
+    assert lib.moat_int4_gemm_tiles(FAKE, FAKE, big, 1, 2048, 2048, ctypes.byref(dot2), big, 1 << 30, None) == I
+    assert lib.moat_int4_gemm_tiles(FAKE, FAKE, big, 33, 2048, 2048, ctypes.byref(opt), big, 1 << 30, None) == I
+
+
+def test_tile_order_python_checks_first():
+    import numpy as np
+    from moat_amd import dequant
+    with pytest.raises(ValueError):
+        dequant.records_to_tiles(np.zeros(21 * 144, np.uint8), 1, 5376 - 128)

@@ -321,3 +321,24 @@ def test_silu_mul_closed_forms():
     want = [0.0, 2.0 / (1.0 + math.exp(-1.0)), -1.0 / (1.0 + math.e), 20.0, 0.0, -3.0 / (1.0 + math.exp(-1.0))]
     assert np.allclose(got, want, rtol=1e-15, atol=1e-15)
     assert abs(got[4]) < 1e-15
+
+
+def test_records_to_tiles_is_the_tile_permutation():
+    """Tile order (row r of 256-column tile j at record j*K + r), pinned by a
+    plain index loop and by decoding: tile j's records hold columns
+    256j .. 256j+255 of W, row by row."""
+    for K, M in ((3, 512), (32, 768), (64, 256)):
+        w = O.synthetic_weights(K, M, 0.05, 3 + K + M)
+        blob = O.quantize_pack_a(w).reshape(-1)
+        tiles = O.records_to_tiles(blob, K, M)
+        assert tiles.shape == blob.shape and tiles.dtype == np.uint8
+        t = M // 256
+        for r in range(K):
+            for j in range(t):
+                src = (r * t + j) * 144
+                dst = (j * K + r) * 144
+                assert np.array_equal(tiles[dst:dst + 144], blob[src:src + 144])
+        wdq = O.decode_superblocks(blob, K * M // 256).reshape(K, M)
+        dec = O.decode_superblocks(tiles, K * M // 256).reshape(t, K, 256)
+        for j in range(t):
+            assert np.array_equal(dec[j].view(np.uint16), wdq[:, 256 * j:256 * (j + 1)].view(np.uint16))
