@@ -284,13 +284,13 @@ int32_t moat_int4_to_f16(const void* src, int32_t src_dtype, int64_t n, uint16_t
  * Both calls take a device workspace, 256-byte aligned, of at least the
  * bytes the size calls below give (sampling: about 2 v + 600 bytes per row;
  * softmax: about 600 bytes per 8192 logits, its table values going to the
- * output buffer; MOAT_ERR_WORKSPACE when missing or short).  It starts with
- * one counter word per row, through which the last of a row's workgroups
- * (one per 8192 logits) takes over the row: zero-fill the workspace once
- * before first use (e.g. with moat_int4_workspace_clear); every call leaves
- * the counters at zero again, so one workspace serves calls of any shape.
- * Calls that share a workspace must not overlap; use a different workspace
- * from the GEMM's.
+ * output buffer; MOAT_ERR_WORKSPACE when missing or short).  It holds the
+ * call's intermediate results and one counter word per row, through which
+ * the last of a row's workgroups (one per 8192 logits) takes over the row;
+ * each call sets them up itself, so the workspace need not be cleared and
+ * serves calls of any shape.  Calls that share a workspace must not
+ * overlap; use a different workspace from the GEMM's (whose counter words
+ * must stay zero).
  */
 
 /* Workspace bytes of a moat_sample_tokens / moat_lut_softmax call over n rows

@@ -106,4 +106,4 @@ class _Workspaces:
 
 
 workspaces = _Workspaces()  # GEMM calls
-sample_workspaces = _Workspaces()  # sampling calls (their own: other counter words)
+sample_workspaces = _Workspaces()  # sampling calls: their own (they rewrite their counter words)

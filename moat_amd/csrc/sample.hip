@@ -35,7 +35,8 @@
 //                    distribution over its last entry, the first entry above
 //                    the row's uniform draw, and the float32 log of its
 //                    full-softmax p.
-// "Last to finish" is a per-row counter in the workspace: the writer wave
+// "Last to finish" is a per-row counter in the workspace (K1 zeroes it; the
+// row's last workgroup leaves it at zero too): the writer wave
 // publishes its results with sc1 stores (written through the per-XCD L2s to
 // the coherence point) and waits for them to complete before a relaxed
 // agent-scope increment; the workgroup that brings the counter to the chunk
@@ -78,7 +79,7 @@ enum SampleMode { kModeProbs = 0, kModeGreedy = 1, kModeSample = 2 };
 
 // Workspace of one call; per row r and chunk c at r * nch + c.
 struct SampleWs {
-  uint32_t* cnt;    // [n] workgroups of the row done (zero between calls)
+  uint32_t* cnt;    // [n] workgroups of the row done (zeroed by K1)
   double* cmax;     // chunk maximum of the raw logits (NaN skipped; -inf if none)
   int* cnan;        // first NaN index in the chunk, or kNone
   int* cfirst;      // first index of the chunk maximum, or kNone
@@ -442,6 +443,9 @@ __global__ void __launch_bounds__(kT) chunk_stats_kernel(const T* __restrict__ x
     publish(ws.cmax + at, best);
     publish(ws.cnan + at, fnan);
     publish(ws.cfirst + at, idx);
+    // the row's counter starts from zero in the launches that follow (only
+    // rows of more than one chunk, which all run K1, use it)
+    if (c == 0) ws.cnt[r] = 0u;
   }
 }
 

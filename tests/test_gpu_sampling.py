@@ -287,3 +287,11 @@ def test_workspace_counters_return_to_zero():
         torch.cuda.synchronize()
         ws = D.sample_workspaces.get(1)
         assert int(torch.count_nonzero(ws[:4 * 9])) == 0, temp
+    # a workspace full of stale bytes: every call sets up its own counters
+    ws.fill_(0xAB)
+    for temp in (0.0, 0.7):
+        tok, lp = sampler.sample_tokens(x, temperature=temp, seed=9)
+        wt, wl = S.sample_tokens(x, temperature=temp, seed=9)
+        assert np.array_equal(tok, wt) and np.array_equal(lp.view(np.uint16 if temp == 0 else np.uint32),
+                                                          wl.view(np.uint16 if temp == 0 else np.uint32))
+        ws.fill_(0xAB)
