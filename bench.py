@@ -438,8 +438,9 @@ def run_sample(args) -> int:
     dom = max(ns)
     roof = {"bound": "hbm", "achieved": per_n[dom]["sample_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(per_n[dom]["sample_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
-            "kernel": (f"sampler (chunk stats, sums, select + draw: 3 launches) N={dom}: {per_n[dom]['sample_bytes']} B per call (fp32 logits, "
-                       f"the 64 KB table, tokens and logs) / {per_n[dom]['sample_us']} us")}
+            "kernel": (f"sampler (chunk stats, sums, select + draw: 3 launches) N={dom}: "
+                       f"{per_n[dom]['sample_bytes']} B per call (fp32 logits, the 64 KB table, tokens and logs) / "
+                       f"{per_n[dom]['sample_us']} us")}
     cpu = None
     if not args.no_cpu_baseline:
         sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
