@@ -111,7 +111,7 @@ def _workspace(n: int, v: int, softmax: bool = False):
 
 def _check_table(exp_lut: ExponentialLUT) -> None:
     if exp_lut.size > MAX_TABLE:
-        raise ValueError(f"table of {exp_lut.size} entries: the GPU softmax holds at most {MAX_TABLE}")
+        raise ValueError(f"table of {exp_lut.size} entries: the GPU softmax indexes at most {MAX_TABLE}")
 
 
 def safe_softmax_lut(x, exp_lut: ExponentialLUT, axis: int = -1):
