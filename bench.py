@@ -175,7 +175,7 @@ def main() -> int:
         return 0
 
     if args.gpus != 1:
-        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})",
+        print(f"bench.py measures one GPU: moat_amd has no multi-GPU path (asked for --gpus {args.gpus})",
               file=sys.stderr)
         return 2
 

@@ -300,7 +300,7 @@ def records_to_tiles(superblocks, K: int, M: int) -> torch.Tensor:
     column order (row r of tile j at record ``j * K + r``).  A GPU uint8
     tensor; :func:`batched_int4_matmul` reads it with ``tile_order=True``,
     with the same result bits and a faster weight stream.  (A storage order
-    of this build; the reference's stream is the row order.)"""
+    with no counterpart in the reference, whose stream is the row order.)"""
     K, M = int(K), int(M)
     if K < 1 or M < 256 or M % 256 != 0:
         raise ValueError(f"tile order needs M % 256 == 0 (got K={K}, M={M})")

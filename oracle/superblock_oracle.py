@@ -261,8 +261,8 @@ def decode_superblocks(blob, num_superblocks: int) -> np.ndarray:
 def records_to_tiles(blob, K: int, M: int) -> np.ndarray:
     """The records of a row-major K x M stream (M % 256 == 0) in tile order:
     record (row r, 256-column tile j) moves from ``r * (M/256) + j`` to
-    ``j * K + r`` (a storage order of this build, no reference counterpart:
-    the records themselves are unchanged)."""
+    ``j * K + r`` (a storage order with no counterpart in the reference; the
+    records themselves are unchanged)."""
     t = M // SB_ELEMS
     rec = np.asarray(blob, dtype=np.uint8).reshape(K, t, SB_BYTES)
     return np.ascontiguousarray(rec.transpose(1, 0, 2)).reshape(-1)
