@@ -278,7 +278,7 @@ int32_t moat_int4_to_f16(const void* src, int32_t src_dtype, int64_t n, uint16_t
  * `lut_f16` is the exp table of ExponentialLUT (attention.py:32-58): lut_size
  * fp16 values of exp over [-range_max, 0], 2 <= lut_size <= 2^24; `step` is
  * range_max / (lut_size - 1) rounded to float32.  Logits are [n][v] of dtype
- * F32, F16 or F64, 0 <= n <= 2^22, 1 <= v <= 524288 (up to 64 chunks of 8192
+ * F32, F16 or F64, 0 <= n <= 2^21, 1 <= v <= 524288 (up to 64 chunks of 8192
  * logits, one workgroup each).
  *
  * Both calls take a device workspace, 256-byte aligned, of at least the

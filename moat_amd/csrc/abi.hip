@@ -272,16 +272,15 @@ int32_t run_fused(int mode, const uint16_t* x, const uint8_t* const* sbs, float*
                                            partials, stream));
 }
 
-// Row count (a row's workgroup index times 1024 threads fits 32 bits) and
-// vocabulary (64 chunks of 8192 logits) of the sampling calls.
+// Row count (rows x 1024 threads, the launches' first grid dimension, stays
+// below 2^32) and vocabulary (64 chunks of 8192 logits) of the sampling calls.
 bool sample_sizes_ok(int32_t n, int32_t v) {
-  return n >= 0 && n <= (1 << 22) && v >= 1 && v <= moat::sample_max_vocab();
+  return n >= 0 && n <= (1 << 21) && v >= 1 && v <= moat::sample_max_vocab();
 }
 
 // Shared checks of the sampling entry points: dtype, 1 <= v <= 524288 (64
 // chunks of 8192 logits), table of 2..2^24 fp16 entries (indices exact in
-// float32), positive finite step, at most 2^22 rows (a row's workgroup
-// index times 1024 threads fits 32 bits).
+// float32), positive finite step, at most 2^21 rows.
 bool sample_args_ok(const void* x, int32_t dtype, int32_t n, int32_t v, const uint16_t* lut, int32_t lut_size,
                     float step) {
   if (dtype != MOAT_DTYPE_F32 && dtype != MOAT_DTYPE_F16 && dtype != MOAT_DTYPE_F64) return false;

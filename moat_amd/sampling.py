@@ -39,7 +39,7 @@ from . import _lib
 MAX_VOCAB = 64 * 8192  # logits per row: 64 chunks of numpy's 8192-element sum pieces
 MAX_TABLE = 1 << 24  # table entries (indices exact in float32)
 MAX_TOP_K = 64
-_MAX_ROWS = 1 << 22  # rows per call
+_MAX_ROWS = 1 << 21  # rows per call (rows x 1024 threads stay below 2^32)
 DEFAULT_TOP_K = 50  # batch_generator.py:241
 
 _DTYPES = {torch.float32: _lib.DTYPE_F32, torch.float16: _lib.DTYPE_F16, torch.float64: _lib.DTYPE_F64}

@@ -188,9 +188,9 @@ def test_sampling_entry_points_validate(lib):
     assert lib.moat_sample_workspace_size(2, 0) == -1 and lib.moat_sample_workspace_size(-1, 10) == -1
     assert lib.moat_sample_workspace_size(1, 524288) > 2 * 524288
     assert lib.moat_sample_workspace_size(1, 524289) == -1 and lib.moat_lut_softmax_workspace_size(1, 524289) == -1
-    assert lib.moat_sample_workspace_size((1 << 22) + 1, 10) == -1
-    big = lib.moat_sample_workspace_size(1 << 22, 1 << 19)  # 64-bit byte counts
-    assert big > 2 * (1 << 22) * (1 << 19)
+    assert lib.moat_sample_workspace_size((1 << 21) + 1, 10) == -1
+    big = lib.moat_sample_workspace_size(1 << 21, 1 << 19)  # 64-bit byte counts
+    assert big > 2 * (1 << 21) * (1 << 19)
 
     # moat_lut_softmax(x, dtype, n, v, lut, lut_size, step, probs, workspace, bytes, stream)
     def sm(x, dtype, n, v, lut_size, st, probs, w=FAKE, nbytes=sws):

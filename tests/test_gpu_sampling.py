@@ -295,3 +295,19 @@ def test_workspace_counters_return_to_zero():
         assert np.array_equal(tok, wt) and np.array_equal(lp.view(np.uint16 if temp == 0 else np.uint32),
                                                           wl.view(np.uint16 if temp == 0 else np.uint32))
         ws.fill_(0xAB)
+
+
+def test_softmax_rows_past_one_call():
+    """More rows than one call takes (2^21): the softmax runs in slices of
+    rows; rows on both sides of the slice boundary and a sample of the rest
+    equal the oracle."""
+    import torch
+    from moat_amd.sampling import ExponentialLUT, safe_softmax_lut, _MAX_ROWS
+    say("case: softmax rows past one call")
+    rows = _MAX_ROWS + 3
+    x = torch.randn((rows, 2), dtype=torch.float32, device="cuda") * 3
+    got = safe_softmax_lut(x, ExponentialLUT()).cpu().numpy()
+    xh = x.cpu().numpy()
+    pick = np.concatenate([np.arange(_MAX_ROWS - 3, rows), np.random.default_rng(4).integers(0, rows, 200)])
+    want = S.softmax_lut(xh[pick], S.exp_table(), S.table_step_f32())
+    assert np.array_equal(got[pick].view(np.uint16), want.view(np.uint16))
