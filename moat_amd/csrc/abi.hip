@@ -104,7 +104,7 @@ bool options_ok(const moat_int4_gemm_options* o, int32_t n) {
 // and share 128-byte lines in L2), about 8 rounds per workgroup, at most one
 // per CU, and a K split whose fp32 partials stay well below the weight stream.
 void plan_records(GemmPlan& p, int32_t n, int32_t k, int64_t groups, int64_t tiles, int group, int waves,
-                  const moat_int4_gemm_options& opt) {
+                  const moat_int4_gemm_options& opt, bool fill_cus) {
   const int rounds = moat::gemm_rounds(k);
   // ring depth (LDS: waves x depth x 7 or 8 KB; the launch clamps it to the LDS)
   const int depth = opt.batch ? opt.batch : (waves == 8 ? 2 : (n <= 16 ? 3 : 2));
@@ -155,8 +155,9 @@ void plan_records(GemmPlan& p, int32_t n, int32_t k, int64_t groups, int64_t til
   // boundaries (a second segment in some workgroups), which costs less than
   // the idle CUs when the weight stream is the bound.  Measured at K=8192 x
   // M=28672 (224 -> 256 workgroups, N = 1..8): 5-9 % faster on the tile
-  // order, unchanged on the row order; slower above 8 rows.
-  if (opt.splits <= 0 && n <= 8 && wgs < 256 && items >= 8 * 256) wgs = 256;
+  // order, unchanged on the row order; slower above 8 rows.  (Single
+  // projections only: the fused launches keep the split count.)
+  if (fill_cus && opt.splits <= 0 && n <= 8 && wgs < 256 && items >= 8 * 256) wgs = 256;
   if (wgs > items) wgs = items;
   // the kernel addresses the partials with 32-bit byte offsets
   const int64_t max_wgs = (int64_t)0xFFFFFFFF / ((int64_t)2 * group * n * 256 * (int64_t)sizeof(float));
@@ -204,7 +205,7 @@ GemmPlan plan_gemm(int32_t n, int32_t k, int32_t m, const moat_int4_gemm_options
     // 8 waves per workgroup only up to 16 rows (the accumulators of 32 rows
     // need more registers than 8 waves leave a lane)
     const int waves = (opt.waves && n <= 16) ? opt.waves : 4;
-    plan_records(p, n, k, moat::gemm_records_groups(m, group), moat::gemm_records_tiles(m), group, waves, opt);
+    plan_records(p, n, k, moat::gemm_records_groups(m, group), moat::gemm_records_tiles(m), group, waves, opt, true);
     return p;
   }
   const int tiles = moat::gemm_col_tiles(m);
@@ -255,7 +256,7 @@ GemmPlan plan_fused(int mode, int32_t count, int32_t n, int32_t k, int32_t m) {
   const int64_t tiles = moat::gemm_records_tiles(m);
   const int group = mode == kFusedSwiglu ? 2 : 1;  // SwiGLU: a gate tile and an up tile per group
   plan_records(p, n, k, moat::gemm_fused_groups(mode, count, m), (mode == kFusedSwiglu ? 2 : count) * tiles, group,
-               4, opt);
+               4, opt, false);
   p.algo = MOAT_GEMM_MFMA;
   return p;
 }
