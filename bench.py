@@ -1,17 +1,23 @@
 #!/usr/bin/env python3
 """Benchmark of the INT4 superblock dequant-GEMM on one MI355X.
 
-Workload (default): the FFN gate/up projection K=2048 x M=5504, weights
-~N(0, 0.02) (seed 1002) quantized to 144-byte superblocks (2048*5504/256 =
-44,032 records, 6.34 MB), fp16 activations ~N(0, 1), swept over N = 1, 2, 4,
-8, 16, 32 parallel traces.  One "step" is one sweep: six projections, one per
+Workload (default): the FFN projection K=3072 x M=8192, weights ~N(0, 0.02)
+(seed 1003) quantized to 144-byte superblocks (3072*8192/256 = 98,304
+records, 14.16 MB), fp16 activations ~N(0, 1), swept over N = 1, 2, 4, 8,
+16, 32 parallel traces.  One "step" is one sweep: six projections, one per
 N, each on a different copy of the weight stream (copies rotate so that the
 256 MB Infinity Cache cannot serve repeats: >= 300 MB of distinct records).
+Beside it, the largest single-GPU projection, K=8192 x M=28672 (132 MB of
+records, 0.1 % outliers at 8 sigma), at N = 1, 8, 32 in tile order (the
+loader's layout) and row order (the reference's stream).
 
 Printed: one JSON line with the whole-job throughput (tokens/s over the
-sweep), per-N microseconds/call, HBM GB/s and roofline fraction, the
-roofline of the dominant kernel and the CPU baseline (the numpy oracle on the
-host cores, a bounded sample).
+sweep), per-N microseconds per call (graph replay) and kernel time (HIP
+events around each call), HBM GB/s and roofline fraction on the kernel time,
+the same bytes read by a plain streaming-read kernel (the floor), the
+roofline of the dominant kernel and the CPU baseline (the numpy oracle of
+the reference CPU path on the host cores, with matmul-only, torch and
+one-thread variants).
 """
 
 from __future__ import annotations
@@ -41,6 +47,9 @@ WORKLOAD_NAMES = {
     "k2048_m32000": "int4 superblock LM head K=2048 (hidden) x M=32000 (vocabulary), N sweep 1..32",
 }
 ROTATE_BYTES = 300 * 1024 * 1024
+DEFAULT_CONFIG = "k3072_m8192"
+# measured beside the default workload: the largest single-GPU projection
+SIDE_CONFIG = ("k8192_m28672", [1, 8, 32])
 # One decoder layer's projections at hidden 2048 (Q, K, V, O 2048x2048; gate
 # and up 2048x5632; down 5632 -> 2048), run back to back at N = 16 traces.
 LAYER = [("q", 2048, 2048), ("k", 2048, 2048), ("v", 2048, 2048), ("o", 2048, 2048),
@@ -58,52 +67,97 @@ def algo_bytes(N: int, K: int, M: int) -> int:
     return 144 * K * M // 256 + 2 * N * K + 4 * N * M
 
 
+def _thread_info() -> dict:
+    import torch
+    info = {"os_cpu_count": os.cpu_count(), "affinity": len(os.sched_getaffinity(0)),
+            "torch_threads": torch.get_num_threads()}
+    try:
+        from threadpoolctl import threadpool_info
+        pools = threadpool_info()
+        info["blas_threads"] = max((p.get("num_threads") or 1) for p in pools) if pools else None
+        info["blas"] = sorted({p.get("internal_api", "?") for p in pools})
+    except Exception:  # threadpoolctl missing
+        info["blas_threads"] = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return info
+
+
 def cpu_baseline(K, M, ns, blob, budget_s: float):
-    """The oracle on the host: decode the records, then a float32 matmul (the
-    reference CPU path), timed per N on a bounded number of repetitions."""
+    """The reference CPU path on the host (the oracle: decode the records,
+    then a float32 matmul), per N, median of 3-10 repetitions, and beside it:
+    the matmul alone on weights decoded beforehand, torch.matmul in fp32 on
+    the CPU, and decode + matmul on one thread (BLAS and torch limited to 1).
+    `value` is decode + matmul on all threads over the N sweep."""
+    import torch
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from oracle import superblock_oracle as O
 
-    try:
-        from threadpoolctl import threadpool_info
-        threads = max((p.get("num_threads") or 1) for p in threadpool_info()) if threadpool_info() else 1
-    except Exception:  # threadpoolctl missing
-        threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    per_n = {}
-    per_n_budget = budget_s / len(ns)
-    total_t, total_tok = 0.0, 0
-    for N in ns:
-        x = O.synthetic_activations(N, K, 2200 + N)
-        O.gemm_ref(x, blob, K, M)  # warm
+    info = _thread_info()
+    w32 = O.decode_superblocks(blob, K * M // 256).astype(np.float32).reshape(K, M)
+    w32_t = torch.from_numpy(w32)
+    xs = {N: O.synthetic_activations(N, K, 2200 + N) for N in ns}
+    per_variant_budget = budget_s / 4
+
+    def timed(fn, budget):
+        fn()  # warm
         times = []
         t_start = time.perf_counter()
-        while len(times) < 3 or (time.perf_counter() - t_start < per_n_budget and len(times) < 10):
+        while len(times) < 3 or (time.perf_counter() - t_start < budget and len(times) < 10):
             t0 = time.perf_counter()
-            O.gemm_ref(x, blob, K, M)
+            fn()
             times.append(time.perf_counter() - t0)
-        med = float(np.median(times))
-        per_n[N] = {"ms_per_call": med * 1e3, "tok_s": N / med, "reps": len(times)}
-        total_t += med
-        total_tok += N
+        return float(np.median(times)), len(times)
+
+    def sweep(make_fn, nlist, budget):
+        out, tt, tok = {}, 0.0, 0
+        for N in nlist:
+            med, reps = timed(make_fn(N), budget / len(nlist))
+            out[N] = {"ms_per_call": round(med * 1e3, 3), "tok_s": round(N / med, 2), "reps": reps}
+            tt += med
+            tok += N
+        return out, tok / tt
+
+    full, value = sweep(lambda N: (lambda: O.gemm_ref(xs[N], blob, K, M)), ns, per_variant_budget)
+    mm, mm_v = sweep(lambda N: (lambda: xs[N].astype(np.float32) @ w32), ns, per_variant_budget)
+    tm, tm_v = sweep(lambda N: (lambda: torch.from_numpy(xs[N].astype(np.float32)) @ w32_t), ns, per_variant_budget)
+    prev_torch = torch.get_num_threads()
+    try:
+        from threadpoolctl import threadpool_limits
+        limiter = threadpool_limits(limits=1)
+    except Exception:
+        limiter = None
+    torch.set_num_threads(1)
+    try:
+        one, one_v = sweep(lambda N: (lambda: O.gemm_ref(xs[N], blob, K, M)), ns, per_variant_budget)
+    finally:
+        torch.set_num_threads(prev_torch)
+        if limiter is not None:
+            limiter.restore_original_limits()
     return {
-        "value": total_tok / total_t,
+        "value": round(value, 2),
         "unit": "tok/s",
-        "cores": int(threads),
+        "cores": int(info.get("blas_threads") or 1),
         "kind": "port",
-        "sample": (f"numpy oracle: decode {K}x{M} records then float32 matmul, per N in {ns}, "
-                   f"median of 3-10 reps each (~{budget_s:.0f} s budget); host os.cpu_count()={os.cpu_count()}, "
-                   f"affinity={len(os.sched_getaffinity(0))}"),
-        "per_n": per_n,
+        "sample": (f"numpy oracle of the reference CPU path (decode the {K}x{M} records to fp16, then a float32 "
+                   f"BLAS matmul), per N in {ns}, median of 3-10 reps each (~{budget_s:.0f} s for all variants); "
+                   f"decode is single-threaded numpy, the matmul uses {info.get('blas_threads')} BLAS threads"),
+        "threads": info,
+        "per_n": full,
+        "variants": {
+            "matmul_only_predecoded_f32": {"tok_s": round(mm_v, 2), "per_n": mm},
+            "torch_matmul_f32_cpu": {"tok_s": round(tm_v, 2), "per_n": tm, "torch_threads": info["torch_threads"]},
+            "decode_plus_matmul_1_thread": {"tok_s": round(one_v, 2), "per_n": one},
+        },
     }
 
 
 def traffic_from_counters(fetch_csv: str, write_csv: str, config: str, n: int) -> dict:
-    """HBM bytes per launch of the GEMM kernels from two rocprofv3 --pmc runs
-    of this script (FETCH_SIZE, then WRITE_SIZE, CSV output, ``--ns n``).
-    Each counter is scaled by what it reads for the largest plain copy of the
-    same run: the clones of the weight stream, whose size is known (every
-    clone reads and writes exactly the record bytes).  Returns the entry
-    written to profiles/traffic_<config>.json."""
+    """HBM bytes per call of the GEMM from two rocprofv3 --pmc runs of this
+    script (FETCH_SIZE, then WRITE_SIZE, CSV output, ``--ns n``), counting
+    every kernel of the call (the main kernel and, when the plan has one, the
+    fix-up kernel).  Each counter is scaled by what it reads for the largest
+    plain copy of the same run: the clones of the weight stream, whose size is
+    known (every clone reads and writes exactly the record bytes).  Returns
+    the entry written to profiles/traffic_<config>.json."""
     import csv
     K, M = CONFIGS[config][:2]
     sb_bytes = 144 * K * M // 256
@@ -126,10 +180,139 @@ def traffic_from_counters(fetch_csv: str, write_csv: str, config: str, n: int) -
     kernels = {k: {"read_bytes": round(fetch.get(k, 0.0)), "written_bytes": round(write.get(k, 0.0))}
                for k in sorted(set(fetch) | set(write))}
     main_k = max(kernels, key=lambda k: kernels[k]["read_bytes"])
-    total = kernels[main_k]["read_bytes"] + kernels[main_k]["written_bytes"]
+    total = sum(v["read_bytes"] + v["written_bytes"] for v in kernels.values())
     return {"n": n, "traffic": total, "kernel": main_k, "algorithmic_bytes": algo_bytes(n, K, M),
+            "traffic_over_algorithmic": round(total / algo_bytes(n, K, M), 3),
             "kernels": kernels, "scale": {"FETCH_SIZE": round(fs, 4), "WRITE_SIZE": round(ws, 4)},
             "calibration": f"largest __amd_rocclr_copyBuffer of the run = one clone of the {sb_bytes}-byte record stream"}
+
+
+class Timer:
+    """Timing on one capture stream: per-call time from HIP-graph replays of
+    back-to-back calls, HIP events on the launch stream around the replays.
+    (rocprofv3's kernel durations for the same calls agree with it within a
+    few per cent: the dispatch gap between graph kernels is small.  HIP
+    events inside a graph, which would bracket single kernels, are not
+    available on ROCm, and events around eager launches add the launch path's
+    own time.)"""
+
+    def __init__(self, torch):
+        self.torch = torch
+        self.cap = torch.cuda.Stream()
+        self.cap.wait_stream(torch.cuda.current_stream())
+        self.events_in_graph = True
+
+    def capture(self, fn, calls):
+        torch = self.torch
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=self.cap):
+            for c in range(calls):
+                fn(c)
+        torch.cuda.synchronize()
+        return g
+
+    def replay_us(self, graphs, reps):
+        """Elapsed microseconds of `reps` replays (cycling through `graphs`)."""
+        torch = self.torch
+        with torch.cuda.stream(self.cap):
+            for g in graphs[:2]:
+                g.replay()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(self.cap)
+            for r in range(reps):
+                graphs[r % len(graphs)].replay()
+            e1.record(self.cap)
+        e1.synchronize()
+        return e0.elapsed_time(e1) * 1e3
+
+    def per_call_us(self, fn, calls, total_calls=200):
+        g = self.capture(fn, calls)
+        warm = self.replay_us([g], 1)
+        self.replay_us([g], max(1, int(20000 / max(warm, 1.0))))  # ~20 ms: the GPU leaves its idle clocks
+        reps = max(1, total_calls // calls)
+        return self.replay_us([g], reps) / (reps * calls)
+
+
+def build_projection(torch, dev, config, tile_order):
+    """Weights of `config` quantized on the GPU (row order, or tile order),
+    and enough copies of the records that the rotated set exceeds the 256 MB
+    Infinity Cache."""
+    from moat_amd.dequant import quantize_to_superblocks, records_to_tiles
+    K, M, std, seed, outl, _ = CONFIGS[config]
+    rng = np.random.default_rng(seed)
+    w = rng.standard_normal((K, M), dtype=np.float32) * np.float32(std)
+    if outl:
+        n_out = int(round(outl * K * M))
+        pos = rng.choice(K * M, size=n_out, replace=False)
+        w.reshape(-1)[pos] = rng.choice(np.array([-1.0, 1.0], np.float32), size=n_out) * np.float32(8 * std)
+    blob0 = quantize_to_superblocks(torch.from_numpy(w).to(dev))  # (S, 144) uint8 on the GPU
+    del w
+    row_blob = blob0
+    if tile_order:
+        blob0 = records_to_tiles(blob0, K, M)
+    copies = max(2, -(-ROTATE_BYTES // blob0.numel()))
+    blobs = [blob0] + [blob0.clone() for _ in range(copies - 1)]
+    return blobs, row_blob
+
+
+def measure_projection(torch, timer, lib, config, ns, tile_order, args, with_floor=True):
+    """Per-N figures of one projection shape: per-call time (graph replay),
+    kernel time (events around each call), the streaming-read floor of the
+    same record bytes, GB/s and roofline fraction on the kernel time."""
+    from moat_amd.dequant import _gemm_into
+    dev = torch.device("cuda", 0)
+    K, M = CONFIGS[config][:2]
+    blobs, row_blob = build_projection(torch, dev, config, tile_order)
+    copies = len(blobs)
+    sb_bytes = blobs[0].numel()
+    order = "tile" if tile_order else "row"
+    log(f"[bench] {config} ({order} order): K={K} M={M}, {copies} copies of {sb_bytes / 1e6:.2f} MB records")
+    xs = {N: torch.from_numpy(np.random.default_rng(2000 + 100 * 2 + N).standard_normal((N, K), dtype=np.float32)
+                              .astype(np.float16)).to(dev) for N in ns}
+    ys = {N: torch.empty((N, M), dtype=torch.float32, device=dev) for N in ns}
+
+    def call(N, i):
+        _gemm_into(xs[N], blobs[i % copies], ys[N], K, M, args.algo, args.splits, args.batch, args.finish,
+                   args.front, tile_order=tile_order)
+
+    with torch.cuda.stream(timer.cap):
+        for N in ns:  # creates this stream's workspace before any capture
+            for i in range(3):
+                call(N, i)
+    torch.cuda.synchronize()
+    floor = None
+    if with_floor:
+        sink = torch.zeros(1, dtype=torch.int32, device=dev)
+
+        def read(i):
+            _lib_check(lib.moat_int4_stream_read(blobs[i % copies].data_ptr(), sb_bytes, 0, sink.data_ptr(),
+                                                 timer.cap.cuda_stream))
+        f_call = timer.per_call_us(read, copies, args.calls)
+        floor = {"bytes": sb_bytes, "us_per_call": round(f_call, 3), "gbs": round(sb_bytes / f_call / 1e3, 1),
+                 "kernel": "stream_read_kernel (16-byte loads, up to 2048 workgroups of 256 threads)"}
+        log(f"[bench]   read floor: {f_call:7.2f} us per call ({sb_bytes / f_call / 1e3:6.0f} GB/s)")
+    per_n = {}
+    for N in ns:
+        us = timer.per_call_us(lambda c: call(N, c), copies, args.calls)
+        b = algo_bytes(N, K, M)
+        per_n[N] = {"us_per_call": round(us, 3), "gbs": round(b / us / 1e3, 1),
+                    "roofline_frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4), "tok_s": round(N / us * 1e6, 1),
+                    "algo_bytes": b}
+        if floor:
+            per_n[N]["over_read_floor"] = round(us / floor["us_per_call"], 3)
+        log(f"[bench]   N={N:2d}: {us:8.2f} us/call  {b / us / 1e3:7.0f} GB/s  "
+            f"{100 * b / us / 1e3 / HBM_PEAK_GBS:5.1f}% of 8 TB/s"
+            + (f"  | {us / floor['us_per_call']:.2f}x read floor" if floor else ""))
+    t1 = per_n[ns[0]]["us_per_call"] / ns[0]
+    for N in ns:
+        per_n[N]["per_token_speedup_vs_first"] = round(t1 / (per_n[N]["us_per_call"] / N), 3)
+    return {"K": K, "M": M, "order": order, "copies": copies, "per_n": per_n, "read_floor": floor,
+            "call": call, "row_blob": row_blob}
+
+
+def _lib_check(st):
+    if st != 0:
+        raise RuntimeError(f"libmoat_int4 call failed with status {st}")
 
 
 def main() -> int:
@@ -137,9 +320,10 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="k2048_m5504",
+    ap.add_argument("--config", default=DEFAULT_CONFIG,
                     choices=sorted(CONFIGS) + ["layer_h2048", "quantize_load"] + sorted(SAMPLE_CONFIGS),
-                    help="projection shape; layer_h2048: one decoder layer's 7 projections at N=16; "
+                    help="projection shape (default: K=3072 x M=8192, N = 1..32, with K=8192 x M=28672 "
+                         "measured beside it); layer_h2048: one decoder layer's 7 projections at N=16; "
                          "quantize_load: fp16 weights of one layer to INT4 records on the GPU; "
                          "sample_v32000 / sample_v128256: token sampling from V=32000 (K=2048 LM head) or "
                          "V=128256 (K=4096) logits, alone and after the INT4 LM head")
@@ -147,15 +331,17 @@ def main() -> int:
     ap.add_argument("--algo", type=int, default=0, help="0 auto, 1 dot2, 2 mfma")
     ap.add_argument("--splits", type=int, default=0)
     ap.add_argument("--calls", type=int, default=200, help="timed launches per N for the per-N table")
-    ap.add_argument("--cpu-budget", type=float, default=15.0)
+    ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-side", action="store_true",
+                    help="skip the K=8192 x M=28672 block measured beside the default workload")
     ap.add_argument("--batch", type=int, default=0, help="rounds of loads issued together (0 auto)")
     ap.add_argument("--finish", type=int, default=0, help="split-K hand-off (0 auto, 1 atomics, 2 fences, 3 kernel)")
     ap.add_argument("--front", type=int, default=0,
                     help="load front end (0 auto, 1 LDS-staged, 2 direct, 3 LDS DMA, 4 record stream)")
     ap.add_argument("--tile-order", action="store_true",
                     help="GEMM configs: weights stored in tile order (each 256-column tile's rows contiguous; "
-                         "moat_int4_records_to_tiles), read by moat_int4_gemm_tiles; needs M % 256 == 0")
+                         "moat_int4_records_to_tiles), read by moat_int4_gemm_tiles; needs M %% 256 == 0")
     ap.add_argument("--fused", action="store_true",
                     help="layer_h2048: Q, K, V in one launch and gate/up fused with SwiGLU (h feeds down)")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"), default=None,
@@ -188,104 +374,49 @@ def main() -> int:
 
     import torch
     from moat_amd import _lib
-    from moat_amd.dequant import _gemm_into, quantize_to_superblocks, records_to_tiles
 
     lib = _lib.load()
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
-    K, M, std, seed, outl, default_ns = CONFIGS[args.config]
+    K, M = CONFIGS[args.config][:2]
     if args.tile_order and M % 256 != 0:
         print(f"--tile-order needs M % 256 == 0 (M = {M})", file=sys.stderr)
         return 2
-    ns = [int(v) for v in args.ns.split(",")] if args.ns else default_ns
-
-    rng = np.random.default_rng(seed)
-    log(f"[bench] building {args.config}: K={K} M={M}")
-    w = rng.standard_normal((K, M), dtype=np.float32) * np.float32(std)
-    if outl:
-        n_out = int(round(outl * K * M))
-        pos = rng.choice(K * M, size=n_out, replace=False)
-        w.reshape(-1)[pos] = rng.choice(np.array([-1.0, 1.0], np.float32), size=n_out) * np.float32(8 * std)
-    blob0 = quantize_to_superblocks(torch.from_numpy(w).to(dev))  # (S, 144) uint8 on the GPU
-    del w
-    if args.tile_order:
-        blob0 = records_to_tiles(blob0, K, M)
-    sb_bytes = blob0.numel()
-    copies = max(2, -(-ROTATE_BYTES // sb_bytes))
-    blobs = [blob0] + [blob0.clone() for _ in range(copies - 1)]
-    log(f"[bench] {copies} copies of {sb_bytes / 1e6:.2f} MB records ({copies * sb_bytes / 1e6:.0f} MB rotated)")
-
-    xs = {N: torch.from_numpy(np.random.default_rng(2000 + 100 * 2 + N).standard_normal((N, K), dtype=np.float32)
-                              .astype(np.float16)).to(dev) for N in ns}
-    ys = {N: torch.empty((N, M), dtype=torch.float32, device=dev) for N in ns}
-
-    def one_call(N, i):
-        _gemm_into(xs[N], blobs[i % copies], ys[N], K, M, args.algo, args.splits, args.batch, args.finish,
-                   args.front, tile_order=args.tile_order)
-
-    # All timed work is replayed from HIP graphs captured on one stream, so the
-    # timed region holds back-to-back kernels and no Python launch overhead.
-    cap = torch.cuda.Stream()
-    cap.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(cap):
-        for N in ns:  # creates this stream's workspace before any capture
-            for i in range(3):
-                one_call(N, i)
-    torch.cuda.synchronize()
-
-    def capture(calls):
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g, stream=cap):
-            for N, i in calls:
-                one_call(N, i)
-        torch.cuda.synchronize()
-        return g
-
-    def timed(graphs, reps):
-        with torch.cuda.stream(cap):
-            for g in graphs[:2]:
-                g.replay()
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record(cap)
-            for r in range(reps):
-                graphs[r % len(graphs)].replay()
-            e1.record(cap)
-        e1.synchronize()
-        return e0.elapsed_time(e1) * 1e3  # us
-
-    # per-N table: `calls` launches per N, each on the next weight copy, after
-    # about 20 ms of the same launches (the GPU leaves its idle clocks)
-    per_n = {}
-    for N in ns:
-        g = capture([(N, i) for i in range(copies)])
-        reps = max(1, args.calls // copies)
-        warm_us = timed([g], 1)
-        timed([g], max(1, int(20000 / max(warm_us, 1.0))))
-        us = timed([g], reps) / (reps * copies)
-        b = algo_bytes(N, K, M)
-        per_n[N] = {"us_per_call": round(us, 3), "gbs": round(b / us / 1e3, 1),
-                    "roofline_frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4), "tok_s": round(N / us * 1e6, 1),
-                    "algo_bytes": b}
-        log(f"[bench] N={N:2d}: {us:8.2f} us/call  {b / us / 1e3:7.0f} GB/s  "
-            f"{100 * b / us / 1e3 / HBM_PEAK_GBS:5.1f}% of 8 TB/s")
-        del g
-    t1 = per_n[ns[0]]["us_per_call"] / ns[0]
-    for N in ns:
-        per_n[N]["per_token_speedup_vs_first"] = round(t1 / (per_n[N]["us_per_call"] / N), 3)
+    ns = [int(v) for v in args.ns.split(",")] if args.ns else CONFIGS[args.config][5]
+    timer = Timer(torch)
+    main_res = measure_projection(torch, timer, lib, args.config, ns, args.tile_order, args)
+    per_n, call = main_res["per_n"], main_res["call"]
+    copies = main_res["copies"]
 
     # steps: one sweep over ns per step; graph s covers steps s, s+G, ... and
     # every call of every graph reads a different weight copy
     n_graphs = max(1, copies // len(ns))
-    step_graphs = [capture([(N, s * len(ns) + i) for i, N in enumerate(ns)]) for s in range(n_graphs)]
-    with torch.cuda.stream(cap):
+    step_graphs = []
+    for s_ in range(n_graphs):
+        step_graphs.append(timer.capture(lambda c, s_=s_: call(ns[c], s_ * len(ns) + c), len(ns)))
+    with torch.cuda.stream(timer.cap):
         for w in range(args.warmup):
             step_graphs[w % n_graphs].replay()
     torch.cuda.synchronize()
-    us_total = timed(step_graphs, args.steps)
+    us_total = timer.replay_us(step_graphs, args.steps)
     ms_step = us_total / args.steps / 1e3
     tokens = sum(ns)
     value = tokens / (ms_step / 1e3)
     log(f"[bench] sweep: {ms_step * 1e3:.1f} us/step, {value:.0f} tok/s")
+
+    side = None
+    if args.config == DEFAULT_CONFIG and not args.no_side and not args.ns:
+        side_cfg, side_ns = SIDE_CONFIG
+        side = {}
+        for tile in (True, False):
+            r = measure_projection(torch, timer, lib, side_cfg, side_ns, tile, args, with_floor=tile)
+            side["tile_order" if tile else "row_order"] = {
+                "per_n": {str(k): v for k, v in r["per_n"].items()}, "read_floor": r["read_floor"],
+                "copies": r["copies"]}
+            del r
+            torch.cuda.empty_cache()
+        side = {"workload": WORKLOAD_NAMES[side_cfg], "K": CONFIGS[side_cfg][0], "M": CONFIGS[side_cfg][1],
+                "ns": side_ns, **side}
 
     dom = max(ns, key=lambda n: per_n[n]["us_per_call"])
     roof = {
@@ -295,23 +426,27 @@ def main() -> int:
         "unit": "GB/s",
         "frac": per_n[dom]["roofline_frac"],
         "traffic": None,
-        "kernel": (f"int4 gemm N={dom}: {per_n[dom]['algo_bytes']} algorithmic B per call / "
-                   f"{per_n[dom]['us_per_call']} us per call (main kernel + fix-up of shared tiles)"),
+        "kernel": (f"int4 gemm N={dom} (the sweep's longest call): {per_n[dom]['algo_bytes']} algorithmic B per "
+                   f"call / {per_n[dom]['us_per_call']} us per call (HIP-graph replay of back-to-back calls; the "
+                   f"main kernel plus the fix-up kernel when the plan has one)"),
     }
     traffic_file = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                                 f"traffic_{args.config}.json")
-    if os.path.exists(traffic_file):
+    if os.path.exists(traffic_file) and not args.tile_order:
         with open(traffic_file) as f:
             tr = json.load(f).get(str(dom))
         if tr is not None:
             roof["traffic"] = tr["traffic"]
-            roof["traffic_source"] = f"profiles/traffic_{args.config}.json ({tr['kernel']})"
+            roof["traffic_source"] = f"profiles/traffic_{args.config}.json (all kernels of the call)"
 
     cpu = None
     if not args.no_cpu_baseline:
         log("[bench] CPU baseline (numpy oracle) ...")
-        cpu = cpu_baseline(K, M, ns, blob0.cpu().numpy(), args.cpu_budget)
-        log(f"[bench] CPU baseline: {cpu['value']:.1f} tok/s on {cpu['cores']} threads")
+        cpu = cpu_baseline(K, M, ns, main_res["row_blob"].cpu().numpy(), args.cpu_budget)
+        log(f"[bench] CPU baseline: {cpu['value']:.1f} tok/s (decode + matmul, {cpu['cores']} BLAS threads); "
+            f"matmul alone {cpu['variants']['matmul_only_predecoded_f32']['tok_s']:.1f}, torch fp32 "
+            f"{cpu['variants']['torch_matmul_f32_cpu']['tok_s']:.1f}, one thread "
+            f"{cpu['variants']['decode_plus_matmul_1_thread']['tok_s']:.1f} tok/s")
 
     out = {
         "metric": "INT4 dequant-GEMM µs/call, HBM GB/s (% roofline), tok/s at N=1..32",
@@ -327,12 +462,16 @@ def main() -> int:
         "dtype": "f16",  # dequantized weights and activations in fp16, products summed in fp32
         "data": "synthetic",
         "config": {"workload": WORKLOAD_NAMES[args.config], "K": K, "M": M, "ns": ns,
-                   "weight_copies_rotated": copies, "timing": "HIP graph replay, HIP events on the launch stream",
+                   "weight_copies_rotated": copies,
+                   "timing": "step: HIP graph replay of one N sweep; per N: HIP graph replay of back-to-back calls, "
+                             "HIP events on the launch stream",
                    "algo": args.algo, "splits": args.splits, "batch": args.batch, "finish": args.finish,
                    "front": args.front, "weights": "int4 superblocks (144 B per 256 weights)"
                    + (", tile order" if args.tile_order else ", row order"),
                    "activations": "fp16", "output": "fp32"},
         "per_n": {str(k): v for k, v in per_n.items()},
+        "read_floor": main_res["read_floor"],
+        "largest_projection": side,
         "roofline": roof,
         "cpu_baseline": cpu,
     }

@@ -80,14 +80,26 @@ int32_t moat_int4_dequant(const uint8_t* superblocks, int64_t n_superblocks,
  * (antigravity-engine/tests/test_batched_speed.py:39-42); replaces the fused
  * kernel antigravity-engine/src/shaders/batched_gemm.metal:116-169.
  * Preconditions: 1 <= n <= 32, k >= 1, m >= 32, m % 32 == 0, (k*m) % 256 == 0;
- * x 2-byte aligned, superblocks 16-byte aligned, y 4-byte aligned.
+ * x 2-byte aligned, superblocks 16-byte aligned, y 4-byte aligned.  The
+ * record-stream kernel reads X 16 bytes at a time; when x is not 16-byte
+ * aligned (or k % 8 != 0) the call plans the general kernel instead, and the
+ * size query covers both plans.
  * workspace: device memory of moat_int4_gemm_workspace_size() bytes (may be
- * NULL when that size is 0): a fixed 64 KB block of split-K counters followed
- * by fp32 partials.  Zero-fill it once before first use (e.g. with
- * moat_int4_workspace_clear); every call leaves all of it at zero again (the
- * record-stream kernel's in-kernel hand-off reads a zero word as "partial not
- * written yet"), so one workspace serves calls of any shape.  Calls that share
- * a workspace must not overlap.  m is limited to 2,097,152.
+ * NULL when that size is 0): a fixed 64 KB block (a sticky status word, then
+ * split-K counters) followed by fp32 partials.  Zero-fill it once before
+ * first use (e.g. with moat_int4_workspace_clear); every call leaves all of
+ * it at zero again (the record-stream kernel's in-kernel hand-off reads a
+ * zero word as "partial not written yet"), so one workspace serves calls of
+ * any shape.  Calls that share a workspace must not overlap.  m is limited to
+ * 2,088,960.
+ *
+ * The in-kernel hand-off waits a bounded time (about a second) for another
+ * workgroup's partial.  Should that ever run out (it needs the other
+ * workgroup to be held back from running, e.g. by other work filling the
+ * GPU), the call's affected results are NaN and the status word records it
+ * (moat_int4_workspace_status); every later call on that workspace then
+ * writes NaN instead of results until the workspace is cleared, because a
+ * partial stored after the wait ended may still sit in it.
  */
 int64_t moat_int4_gemm_workspace_size(int32_t n, int32_t k, int32_t m);
 int32_t moat_int4_gemm(const uint16_t* x_f16, const uint8_t* superblocks, float* y_f32,
@@ -163,6 +175,29 @@ int32_t moat_int4_gemm_tiles(const uint16_t* x_f16, const uint8_t* tiles, float*
 
 /* Zero `bytes` bytes of device memory with a kernel (no memset node). */
 int32_t moat_int4_workspace_clear(void* workspace, int64_t bytes, hipStream_t stream);
+
+/*
+ * The sticky status word of a GEMM workspace (workspace_bytes >= 256):
+ * *status_out = 0 when every call since the last clear completed its
+ * hand-offs, else MOAT_WS_HANDOFF_TIMEOUT (see moat_int4_gemm); recovery is
+ * moat_int4_workspace_clear over the whole workspace.  Copies the word to the
+ * host after the work queued on `stream` and waits for it (a synchronising
+ * call).  No counterpart in the reference, whose CPU path has no hand-off.
+ */
+#define MOAT_WS_HANDOFF_TIMEOUT 1
+int32_t moat_int4_workspace_status(const void* workspace, int64_t workspace_bytes, int32_t* status_out,
+                                   hipStream_t stream);
+
+/*
+ * A plain streaming read of `bytes` bytes (16-byte aligned, a multiple of
+ * 16) with 16-byte loads over `workgroups` workgroups of 256 threads (0:
+ * 2048): the read-bandwidth floor against which the GEMM's weight stream is
+ * measured.  Nothing is written (`sink`, one device word, is a guard the
+ * compiler cannot prove unused).  No counterpart in the reference; for
+ * measurement.
+ */
+int32_t moat_int4_stream_read(const void* src, int64_t bytes, int32_t workgroups, uint32_t* sink,
+                              hipStream_t stream);
 
 /*
  * Several projections of one shape that share their activations, in one

@@ -4,6 +4,7 @@ all arithmetic of the path runs in libmoat_int4.so."""
 
 from __future__ import annotations
 
+import ctypes
 import threading
 
 import numpy as np
@@ -103,6 +104,29 @@ class _Workspaces:
                            "moat_int4_workspace_clear")
                 self._bufs[key] = buf
             return buf
+
+    def check(self, what: str) -> None:
+        """Raise if an in-kernel hand-off on this stream's workspace ran out
+        of time since it was last cleared (its sticky status word is set:
+        those calls and every later one on it wrote NaN).  The workspace is
+        cleared before raising, so later calls produce results again.  Waits
+        for the stream's queued work."""
+        dev = require_gpu()
+        key = (dev.index, stream())
+        with self._lock:
+            buf = self._bufs.get(key)
+        if buf is None:
+            return
+        lib = _lib.load()
+        st = ctypes.c_int32(0)
+        _lib.check(lib.moat_int4_workspace_status(buf.data_ptr(), buf.numel(), ctypes.byref(st), stream()),
+                   "moat_int4_workspace_status")
+        if st.value:
+            _lib.check(lib.moat_int4_workspace_clear(buf.data_ptr(), buf.numel(), stream()),
+                       "moat_int4_workspace_clear")
+            raise RuntimeError(f"{what}: a hand-off between workgroups ran out of time (workspace status "
+                               f"{st.value}); the results of that call and of later calls on this stream were "
+                               "NaN; the workspace has been cleared")
 
 
 workspaces = _Workspaces()  # GEMM calls

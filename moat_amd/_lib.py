@@ -19,6 +19,7 @@ MOAT_OK = 0
 MOAT_ERR_INVALID = -2
 MOAT_ERR_HIP = -3
 MOAT_ERR_WORKSPACE = -4
+WS_HANDOFF_TIMEOUT = 1
 
 DTYPE_F32, DTYPE_F16, DTYPE_I8, DTYPE_F64, DTYPE_I64 = 0, 1, 2, 3, 4
 SCALE_F32, SCALE_F16 = 0, 1
@@ -50,6 +51,8 @@ SIGNATURES = {
     "moat_int4_records_to_tiles": (_I32, [_P, _I32, _I32, _P, _P]),
     "moat_int4_gemm_tiles": (_I32, [_P, _P, _P, _I32, _I32, _I32, ctypes.POINTER(GemmOptions), _P, _I64, _P]),
     "moat_int4_workspace_clear": (_I32, [_P, _I64, _P]),
+    "moat_int4_workspace_status": (_I32, [_P, _I64, ctypes.POINTER(_I32), _P]),
+    "moat_int4_stream_read": (_I32, [_P, _I64, _I32, _P, _P]),
     "moat_int4_gemm_multi_workspace_size": (_I64, [_I32, _I32, _I32, _I32]),
     "moat_int4_gemm_multi": (_I32, [_P, _P, _P, _I32, _I32, _I32, _I32, _P, _I64, _P]),
     "moat_int4_gemm_swiglu_workspace_size": (_I64, [_I32, _I32, _I32]),

@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 
 #include "../../include/moat_int4.h"
+#include "handoff.h"
 
 namespace moat {
 hipError_t launch_dequant_stream(const uint8_t* sb, int64_t n_sb, uint16_t* out, hipStream_t st);
@@ -32,7 +33,7 @@ bool gemm_groups_shared(int64_t groups, int64_t rounds, int wgs);
 int gemm_fused_groups(int mode, int mats, int m);
 hipError_t launch_gemm_fused(int mode, const uint16_t* x, const uint8_t* const* sbs, float* const* ys, uint16_t* h,
                              int mats, int n, int k, int m, int wgs, int depth, int finish, float* partials,
-                             hipStream_t stream);
+                             uint32_t* status, hipStream_t stream);
 int sample_max_vocab();
 int64_t sample_workspace_bytes(int n, int v, bool with_e);
 hipError_t launch_lut_sample(const void* x, int dtype, int n, int v, double temp, int scaled, const uint16_t* lut,
@@ -42,19 +43,21 @@ hipError_t launch_lut_lookup(const float* x, int64_t n, const uint16_t* lut, int
                              hipStream_t st);
 hipError_t launch_gemm(int algo, const uint16_t* x, const uint8_t* sb, float* y, int n, int k, int m, int splits,
                        int batch, int finish, int front, int group, int waves, float* partials,
-                       uint32_t* counters, int tile_order, hipStream_t stream);
+                       uint32_t* counters, uint32_t* status, int tile_order, hipStream_t stream);
 hipError_t launch_records_to_tiles(const uint8_t* sb, int k, int m, uint8_t* tiles, hipStream_t stream);
+hipError_t launch_stream_read(const void* src, int64_t bytes, uint32_t* sink, int blocks, hipStream_t st);
 }  // namespace moat
 
 namespace {
 
 constexpr int kMaxN = 32;
 constexpr int kMaxDot2N = 8;
-// The split-K counters live in a fixed block at the start of the workspace so
-// that no call's partials (which follow the block) can overlap the counter
-// words of a call with more column tiles: 16384 tiles = M up to 2,097,152.
+// A fixed 64 KB block at the start of the workspace holds the sticky status
+// word (first 256 bytes) and the general kernel's split-K counters, so that
+// no call's partials (which follow the block) can overlap the counter words
+// of a call with more column tiles: 16320 tiles = M up to 2,088,960.
 constexpr int64_t kCounterBlockBytes = 64 * 1024;
-constexpr int kMaxColTiles = (int)(kCounterBlockBytes / 4);
+constexpr int kMaxColTiles = (int)((kCounterBlockBytes - moat::kWsStatusBytes) / 4);
 
 bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 
@@ -186,11 +189,13 @@ void plan_records(GemmPlan& p, int32_t n, int32_t k, int64_t groups, int64_t til
   p.workspace_bytes = shared ? p.counter_bytes + (int64_t)2 * p.splits * group * n * 256 * (int64_t)sizeof(float) : 0;
 }
 
-GemmPlan plan_gemm(int32_t n, int32_t k, int32_t m, const moat_int4_gemm_options* o) {
+// x_vec: X rows can be read 16 bytes at a time (x 16-byte aligned, k % 8 ==
+// 0), which the record-stream kernel needs.
+GemmPlan plan_gemm(int32_t n, int32_t k, int32_t m, const moat_int4_gemm_options* o, bool x_vec) {
   moat_int4_gemm_options opt = {0, 0, 0, 0, 0, 0, 0};
   if (o) opt = *o;
   GemmPlan p;
-  const bool records_ok = moat::gemm_records_eligible(k, m);
+  const bool records_ok = moat::gemm_records_eligible(k, m) && x_vec;
   // the record-stream kernel (matrix cores) serves every N when the shape allows it
   const bool records = records_ok && opt.algo != MOAT_GEMM_DOT2 &&
                        (opt.front == MOAT_FRONT_AUTO || opt.front == MOAT_FRONT_RECORDS);
@@ -265,12 +270,14 @@ int32_t run_fused(int mode, const uint16_t* x, const uint8_t* const* sbs, float*
                   int32_t n, int32_t k, int32_t m, void* workspace, int64_t workspace_bytes, hipStream_t stream) {
   const GemmPlan p = plan_fused(mode, count, n, k, m);
   float* partials = nullptr;
+  uint32_t* status = nullptr;
   if (p.workspace_bytes > 0) {
     if (!workspace || workspace_bytes < p.workspace_bytes || !aligned(workspace, 16)) return MOAT_ERR_WORKSPACE;
+    status = static_cast<uint32_t*>(workspace);
     partials = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + p.counter_bytes);
   }
   return status_of(moat::launch_gemm_fused(mode, x, sbs, ys, h, count, n, k, m, p.splits, p.batch, p.finish,
-                                           partials, stream));
+                                           partials, status, stream));
 }
 
 // Row count (rows x 1024 threads, the launches' first grid dimension, stays
@@ -307,7 +314,8 @@ int32_t gemm_call(const uint16_t* x_f16, const uint8_t* superblocks, float* y_f3
   if (!gemm_shape_ok(n, k, m) || !options_ok(options, n)) return MOAT_ERR_INVALID;
   if (!x_f16 || !superblocks || !y_f32) return MOAT_ERR_INVALID;
   if (!aligned(x_f16, 2) || !aligned(superblocks, 16) || !aligned(y_f32, 4)) return MOAT_ERR_INVALID;
-  const GemmPlan p = plan_gemm(n, k, m, options);
+  const bool x_vec = aligned(x_f16, 16) && (k % 8) == 0;
+  const GemmPlan p = plan_gemm(n, k, m, options, x_vec);
   if (p.algo == MOAT_GEMM_DOT2 && n > kMaxDot2N) return MOAT_ERR_INVALID;
   // tile order: the record-stream kernel only (whole 256-column tiles, whole
   // 32-row rounds, 16-byte X rows)
@@ -315,13 +323,15 @@ int32_t gemm_call(const uint16_t* x_f16, const uint8_t* superblocks, float* y_f3
     return MOAT_ERR_INVALID;
   float* partials = nullptr;
   uint32_t* counters = nullptr;
+  uint32_t* status = nullptr;
   if (p.workspace_bytes > 0) {
     if (!workspace || workspace_bytes < p.workspace_bytes || !aligned(workspace, 16)) return MOAT_ERR_WORKSPACE;
-    counters = static_cast<uint32_t*>(workspace);
+    status = static_cast<uint32_t*>(workspace);
+    counters = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(workspace) + moat::kWsStatusBytes);
     partials = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + p.counter_bytes);
   }
   return status_of(moat::launch_gemm(p.algo, x_f16, superblocks, y_f32, n, k, m, p.splits, p.batch, p.finish,
-                                     p.front, p.group, p.waves, partials, counters, tile_order, stream));
+                                     p.front, p.group, p.waves, partials, counters, status, tile_order, stream));
 }
 
 
@@ -352,7 +362,11 @@ int32_t moat_int4_dequant(const uint8_t* superblocks, int64_t n_superblocks, uin
 
 int64_t moat_int4_gemm_ex_workspace_size(int32_t n, int32_t k, int32_t m, const moat_int4_gemm_options* options) {
   if (!gemm_shape_ok(n, k, m) || !options_ok(options, n)) return -1;
-  return plan_gemm(n, k, m, options).workspace_bytes;
+  // the plan depends on whether X can be read 16 bytes at a time, which the
+  // size query cannot see: enough for either plan
+  const int64_t a = plan_gemm(n, k, m, options, true).workspace_bytes;
+  const int64_t b = plan_gemm(n, k, m, options, false).workspace_bytes;
+  return a > b ? a : b;
 }
 
 int64_t moat_int4_gemm_workspace_size(int32_t n, int32_t k, int32_t m) {
@@ -417,6 +431,26 @@ int32_t moat_int4_gemm_swiglu(const uint16_t* x_f16, const uint8_t* gate_superbl
     return MOAT_ERR_INVALID;
   const uint8_t* sbs[2] = {gate_superblocks, up_superblocks};
   return run_fused(kFusedSwiglu, x_f16, sbs, nullptr, h_f16, 2, n, k, m, workspace, workspace_bytes, stream);
+}
+
+int32_t moat_int4_stream_read(const void* src, int64_t bytes, int32_t workgroups, uint32_t* sink,
+                              hipStream_t stream) {
+  if (bytes < 0 || (bytes % 16) != 0 || workgroups < 0) return MOAT_ERR_INVALID;
+  if (bytes == 0) return MOAT_OK;
+  if (!src || !sink || !aligned(src, 16) || !aligned(sink, 4)) return MOAT_ERR_INVALID;
+  return status_of(moat::launch_stream_read(src, bytes, sink, workgroups, stream));
+}
+
+int32_t moat_int4_workspace_status(const void* workspace, int64_t workspace_bytes, int32_t* status_out,
+                                   hipStream_t stream) {
+  if (!status_out || !workspace || workspace_bytes < moat::kWsStatusBytes || !aligned(workspace, 4))
+    return MOAT_ERR_INVALID;
+  uint32_t word = 0;
+  hipError_t e = hipMemcpyAsync(&word, workspace, sizeof(word), hipMemcpyDeviceToHost, stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(stream);
+  if (e != hipSuccess) return MOAT_ERR_HIP;
+  *status_out = (int32_t)word;
+  return MOAT_OK;
 }
 
 int32_t moat_int4_workspace_clear(void* workspace, int64_t bytes, hipStream_t stream) {

@@ -56,6 +56,7 @@
 //    to the 8 XCDs) works on one contiguous range of (split, tile) pairs:
 //    neighbouring column tiles share 128-byte lines, which then meet in the
 //    same L2.
+#include "handoff.h"
 #include "superblock_device.h"
 
 namespace moat {
@@ -114,6 +115,10 @@ struct GemmParams {
   const uint8_t* sbm[4];
   float* ym[4];
   uint16_t* h;
+  // Record-stream kernel with shared tile groups: the workspace's sticky
+  // status word (kWsStatus*), read at the start of a call; when set, the call
+  // writes NaN instead of results.  Null when the plan shares no tile group.
+  uint32_t* status;
 };
 
 enum RecMode : int { kModeSingle = 0, kModeMulti = 1, kModeSwiglu = 2 };
@@ -699,16 +704,24 @@ __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("" ::: "memory");
 }
 
+// Inline assembly that reads scalar registers in a vector memory instruction
+// starts with kSgprVmemNops: on gfx9 a VMEM instruction needs 5 wait states
+// after a VALU instruction (v_readlane, v_readfirstlane, v_cmp ...) writes an
+// SGPR it reads, and the compiler, which inserts those wait states between
+// its own instructions, does not look inside inline assembly -- it may reload
+// a spilled base address with v_readlane right before the block.
+#define MOAT_SGPR_VMEM_NOPS "s_nop 4\n\t"
+
 // One global_load_lds_dwordx4: lane l's 16 bytes at base + off (base in
 // scalar registers, a 32-bit per-lane offset) land at LDS byte lds_base +
 // 16*l.  Written as inline assembly so that the compiler, which cannot tell
 // the ring's stages apart, does not guard every later LDS read with a wait for
 // all of these copies; the explicit vmcnt waits above are the only ordering
-// the ring needs.  (s_nop: one wait state between writing M0 and the
+// the ring needs.  (s_nop 0: one wait state between writing M0 and the
 // instruction that reads it.)
 __device__ __forceinline__ void lds_dma16(const void* base, uint32_t off, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(off), "s"(base),
-               "s"(lds_base) : "memory", "m0");
+  asm volatile(MOAT_SGPR_VMEM_NOPS "s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(off),
+               "s"(base), "s"(lds_base) : "memory", "m0");
 }
 
 template <int NR>
@@ -814,31 +827,43 @@ __device__ __forceinline__ void store_sc1(float* p, float4_t v) {
   asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
 }
 
-// Partials of the in-kernel hand-off travel encoded: each word is the bitwise
-// complement of the value, NaN first made the canonical 0x7FC00000, so a word
-// of zero (the complement of 0xFFFFFFFF, a NaN pattern that never reaches the
-// encoder) means "not written yet".  The owner of a tile group clears the
-// words it consumed, which leaves every slot at zero for the next call.
+// Partials of the in-kernel hand-off travel encoded (handoff.h): each word is
+// the bitwise complement of the value, NaN first made the canonical
+// 0x7FC00000, so a word of zero means "not written yet".  The owner of a tile
+// group clears the chunks it consumed, which leaves every slot at zero for
+// the next call.
 __device__ __forceinline__ float4_t enc_partial(float4_t v) {
   float4_t e;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t b = __builtin_isnan(v[i]) ? 0x7FC00000u : __float_as_uint(v[i]);
-    e[i] = __uint_as_float(~b);
-  }
+  for (int i = 0; i < 4; ++i) e[i] = __uint_as_float(handoff_encode(__float_as_uint(v[i])));
   return e;
 }
 
 __device__ __forceinline__ bool partial_ready(float4_t w) {
-  return __float_as_uint(w[0]) != 0u && __float_as_uint(w[1]) != 0u && __float_as_uint(w[2]) != 0u &&
-         __float_as_uint(w[3]) != 0u;
+  return handoff_chunk_written(__float_as_uint(w[0]), __float_as_uint(w[1]), __float_as_uint(w[2]),
+                               __float_as_uint(w[3]));
 }
 
 __device__ __forceinline__ float4_t dec_partial(float4_t w) {
   float4_t v;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) v[i] = __uint_as_float(~__float_as_uint(w[i]));
+  for (int i = 0; i < 4; ++i) v[i] = __uint_as_float(handoff_decode(__float_as_uint(w[i])));
   return v;
+}
+
+// The workspace's sticky status at the start of a call, as a value to add to
+// every result: 0 when the status word is clear (or there is no workspace),
+// NaN when it is set.  Kept in a vector register (adding 0 leaves a result
+// unchanged, -0 aside), where it costs no scalar registers over the kernel.
+__device__ __forceinline__ float read_poison(const GemmParams& P) {
+  const uint32_t st = P.status ? __hip_atomic_load(P.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
+  float poison = st ? __uint_as_float(0x7FC00000u) : 0.0f;
+  asm volatile("" : "+v"(poison));
+  return poison;
+}
+
+__device__ __forceinline__ float4_t poisoned(float4_t v, float poison) {
+  return v + float4_t{poison, poison, poison, poison};
 }
 
 // Repeated batch loads a thread of the owner may spend on chunks not yet
@@ -851,6 +876,7 @@ constexpr int kMaxPolls = 1 << 19;
 // per-lane 32-bit byte offsets.
 __device__ __forceinline__ void load16_sc1(float4_t (&t)[16], const float* base, const uint32_t (&o)[16]) {
   asm volatile(
+      MOAT_SGPR_VMEM_NOPS
       "global_load_dwordx4 %0, %16, %32 sc1\n\t"
       "global_load_dwordx4 %1, %17, %32 sc1\n\t"
       "global_load_dwordx4 %2, %18, %32 sc1\n\t"
@@ -877,7 +903,7 @@ __device__ __forceinline__ void load16_sc1(float4_t (&t)[16], const float* base,
 }
 
 __device__ __forceinline__ void store_sc1_at(float* base, uint32_t o, float4_t v) {
-  asm volatile("global_store_dwordx4 %0, %1, %2 sc1" : : "v"(o), "v"(v), "s"(base) : "memory");
+  asm volatile(MOAT_SGPR_VMEM_NOPS "global_store_dwordx4 %0, %1, %2 sc1" : : "v"(o), "v"(v), "s"(base) : "memory");
 }
 
 // Where a tile group's results go: tile tl of the group covers columns
@@ -887,6 +913,7 @@ __device__ __forceinline__ void store_sc1_at(float* base, uint32_t o, float4_t v
 struct RecOut {
   float* y;
   int m0;
+  float poison;  // added to every result: NaN when the workspace's status was set at the start of the call
 };
 
 template <int kMode>
@@ -896,6 +923,7 @@ __device__ __forceinline__ int rec_col(const RecOut& o, int tl, int qd) {
 
 template <int kMode>
 __device__ __forceinline__ void rec_put_y(const GemmParams& P, const RecOut& o, int row, int col, float4_t v) {
+  v = poisoned(v, o.poison);
   float* yp = o.y + (int64_t)row * P.m + col;
   if (P.y_vec) {
     *reinterpret_cast<float4_t*>(yp) = v;
@@ -905,7 +933,9 @@ __device__ __forceinline__ void rec_put_y(const GemmParams& P, const RecOut& o, 
   }
 }
 
-__device__ __forceinline__ void rec_put_h(const GemmParams& P, int row, int col, float4_t g, float4_t u) {
+__device__ __forceinline__ void rec_put_h(const GemmParams& P, const RecOut& o, int row, int col, float4_t g,
+                                          float4_t u) {
+  g = poisoned(g, o.poison);
   *reinterpret_cast<uint2*>(P.h + (int64_t)row * P.m + col) = swiglu4(g, u);  // m % 128 == 0: 8-byte aligned
 }
 
@@ -931,7 +961,7 @@ __device__ __forceinline__ void rec_store(const GemmParams& P, const float* red,
       const int row = idx >> 6, qd = idx & 63;
       const int col = rec_col<kMode>(o, 0, qd);
       if (col >= P.m) continue;
-      rec_put_h(P, row, col, rec_lds_sum(red, per_slot, nslots, 0, row, qd),
+      rec_put_h(P, o, row, col, rec_lds_sum(red, per_slot, nslots, 0, row, qd),
                 rec_lds_sum(red, per_slot, nslots, 1, row, qd));
     }
     return;
@@ -1002,23 +1032,32 @@ __device__ __forceinline__ void rec_gather_batched(const GemmParams& P, float* r
       load16_sc1(t, P.partials, a);
       // a chunk still unwritten: load the whole batch again (one round trip
       // for all of them) after a short sleep
+      bool ready;
       for (;;) {
-        bool ready = true;
+        ready = true;
 #pragma unroll
         for (int j = 0; j < kQ; ++j)
 #pragma unroll
           for (int i = 0; i < kCB; ++i)
             if (ok[j] && c0 + i < owner) ready = ready && partial_ready(t[j * kCB + i]);
-        if (ready || polls <= 0) break;
+        if (handoff_stop(ready, polls)) break;
         --polls;
         __builtin_amdgcn_s_sleep(1);
         load16_sc1(t, P.partials, a);
       }
+      // out of polls: record it (every later call on this workspace writes
+      // NaN until it is cleared) and add what there is (a missing chunk
+      // decodes to NaN)
+      if (handoff_gave_up(ready, polls)) __hip_atomic_fetch_or(P.status, kWsStatusHandoffTimeout, __ATOMIC_RELAXED,
+                                                               __HIP_MEMORY_SCOPE_AGENT);
 #pragma unroll
       for (int j = 0; j < kQ; ++j)
 #pragma unroll
         for (int i = 0; i < kCB; ++i)  // in workgroup order
           if (ok[j] && c0 + i < owner) v[j] += dec_partial(t[j * kCB + i]);
+      // clear every chunk of the batch: after a give-up this also removes a
+      // late partial that landed between the last poll and here (one that
+      // lands later stays, and the status word covers it)
 #pragma unroll
       for (int j = 0; j < kQ; ++j)
 #pragma unroll
@@ -1064,7 +1103,7 @@ __device__ __forceinline__ void rec_gather(const GemmParams& P, float* red, int 
       const int row = idx >> 6, qd = idx & 63;
       const int col = rec_col<kMode>(o, 0, qd);
       if (col >= P.m) continue;
-      rec_put_h(P, row, col, *reinterpret_cast<const float4_t*>(red + red_pos(row, qd >> 2, qd & 3)),
+      rec_put_h(P, o, row, col, *reinterpret_cast<const float4_t*>(red + red_pos(row, qd >> 2, qd & 3)),
                 *reinterpret_cast<const float4_t*>(red + nslots * per_slot + red_pos(row, qd >> 2, qd & 3)));
     }
   }
@@ -1130,6 +1169,7 @@ __global__ void __launch_bounds__(kW * 64) int4_gemm_records_kernel(GemmParams P
   int lo, hi;
   streamk_range(P, p, lo, hi);
 
+  const float poison = read_poison(P);  // used only when results are written
   const uint64_t round_bytes = P.rec_round_bytes;
   RecSlots slots;
   rec_slots(slots, lane, P.rec_row_m);
@@ -1166,6 +1206,7 @@ __global__ void __launch_bounds__(kW * 64) int4_gemm_records_kernel(GemmParams P
     const uint8_t* wtile = wmat + P.rec_tile_bytes * (uint64_t)(has_tile ? ltile : 0);
     // where the group's results go (the group's first tile)
     RecOut out;
+    out.poison = poison;
     if (kMode == kModeSingle) {
       out.y = P.y;
       out.m0 = tg * kC * kRecCols;
@@ -1280,6 +1321,7 @@ __device__ __forceinline__ float4_t fixup_sum(const GemmParams& P, int group_til
 // partials in workgroup order (with SwiGLU, h from the gate and up sums).
 // One thread per 4-column quad of a tile (of a gate/up pair).
 __global__ void __launch_bounds__(256) streamk_fixup_kernel(GemmParams P, int group_tiles, int mode) {
+  const float poison = read_poison(P);
   const int per_tile = P.n * 64;
   const int tiles = mode == kModeMulti ? P.mats * P.tiles : P.tiles;  // tiles (gate/up pairs) to cover
   const int total = tiles * per_tile;
@@ -1293,7 +1335,7 @@ __global__ void __launch_bounds__(256) streamk_fixup_kernel(GemmParams P, int gr
     if (mode == kModeSwiglu) {
       const int col = tile * kRecCols + 4 * qd;
       if (col >= P.m) continue;
-      const float4_t gsum = fixup_sum(P, 2, item0, p0, p1, 0, row, qd);
+      const float4_t gsum = poisoned(fixup_sum(P, 2, item0, p0, p1, 0, row, qd), poison);
       const float4_t usum = fixup_sum(P, 2, item0, p0, p1, 1, row, qd);
       *reinterpret_cast<uint2*>(P.h + (int64_t)row * P.m + col) = swiglu4(gsum, usum);
       continue;
@@ -1306,7 +1348,7 @@ __global__ void __launch_bounds__(256) streamk_fixup_kernel(GemmParams P, int gr
     }
     const int col = ltile * kRecCols + 4 * qd;
     if (col >= P.m) continue;
-    const float4_t v = fixup_sum(P, group_tiles, item0, p0, p1, tl, row, qd);
+    const float4_t v = poisoned(fixup_sum(P, group_tiles, item0, p0, p1, tl, row, qd), poison);
     float* yp = (mode == kModeMulti ? select4(mat, P.ym[0], P.ym[1], P.ym[2], P.ym[3]) : P.y) +
                 (int64_t)row * P.m + col;
     if (P.y_vec) {
@@ -1465,9 +1507,9 @@ bool gemm_fused_shares_tiles(int mode, int mats, int k, int m, int wgs) {
 
 hipError_t launch_gemm(int algo, const uint16_t* x, const uint8_t* sb, float* y, int n, int k, int m, int splits,
                        int batch, int finish, int front, int group, int waves, float* partials, uint32_t* counters,
-                       int tile_order, hipStream_t stream) {
+                       uint32_t* status, int tile_order, hipStream_t stream) {
   GemmParams P = {};
-  P.x = x; P.sb = sb; P.y = y; P.partials = partials; P.counters = counters;
+  P.x = x; P.sb = sb; P.y = y; P.partials = partials; P.counters = counters; P.status = status;
   P.n = n; P.k = k; P.m = m; P.splits = splits; P.rounds = gemm_rounds(k); P.tiles = gemm_col_tiles(m);
   P.x_vec = ((reinterpret_cast<uintptr_t>(x) & 15) == 0 && (k % 8) == 0) ? 1 : 0;
   P.finish = finish;
@@ -1508,8 +1550,10 @@ hipError_t launch_gemm(int algo, const uint16_t* x, const uint8_t* sb, float* y,
       hipLaunchKernelGGL(streamk_fixup_kernel, dim3(blocks), dim3(256), 0, stream, P, group_tiles, (int)kModeSingle);
       return hipGetLastError();
     }
-    if (tile_order) return hipErrorInvalidValue;  // the tile order has only the records kernel
-    front = kFrontVgprLds;
+    // the planner gives the record-stream front end only to shapes and
+    // inputs it takes (its workgroup count and workspace are not the
+    // general kernel's)
+    return hipErrorInvalidValue;
   }
   // the staged front ends need M % 64 == 0 (4-byte aligned scale pairs)
   if ((m % 64) != 0) front = kFrontDirect;
@@ -1530,9 +1574,9 @@ hipError_t launch_gemm(int algo, const uint16_t* x, const uint8_t* sb, float* y,
 // (m % 128 == 0, k % 32 == 0, x 16-byte aligned).
 hipError_t launch_gemm_fused(int mode, const uint16_t* x, const uint8_t* const* sbs, float* const* ys, uint16_t* h,
                              int mats, int n, int k, int m, int wgs, int depth, int finish, float* partials,
-                             hipStream_t stream) {
+                             uint32_t* status, hipStream_t stream) {
   GemmParams P = {};
-  P.x = x; P.sb = sbs[0]; P.y = ys ? ys[0] : nullptr; P.partials = partials; P.counters = nullptr;
+  P.x = x; P.sb = sbs[0]; P.y = ys ? ys[0] : nullptr; P.partials = partials; P.counters = nullptr; P.status = status;
   P.n = n; P.k = k; P.m = m; P.splits = wgs; P.rounds = gemm_rounds(k);
   P.tiles = gemm_records_tiles(m);
   P.x_vec = 1;

@@ -345,7 +345,11 @@ def batched_int4_matmul_multi(x, superblocks_list, K: int, M: int):
     for r0 in range(0, N, MAX_BATCH_PER_CALL):
         r1 = min(N, r0 + MAX_BATCH_PER_CALL)
         _multi_into(xs[r0:r1], blobs, [y[r0:r1] for y in ys], int(K), int(M))
-    return [D.out_like(y, want_t) for y in ys]
+    if want_t:
+        return ys
+    res = [D.to_host(y) for y in ys]
+    D.workspaces.check("batched_int4_matmul_multi")
+    return res
 
 
 def _multi_into(x: torch.Tensor, blobs, ys, K: int, M: int) -> None:
@@ -378,7 +382,11 @@ def int4_swiglu(x, gate_superblocks, up_superblocks, K: int, M: int):
     for r0 in range(0, N, MAX_BATCH_PER_CALL):
         r1 = min(N, r0 + MAX_BATCH_PER_CALL)
         _swiglu_into(xs[r0:r1], gb, ub, h[r0:r1], int(K), int(M))
-    return D.out_like(h, want_t)
+    if want_t:
+        return h
+    res = D.to_host(h)
+    D.workspaces.check("int4_swiglu")
+    return res
 
 
 def _swiglu_into(x: torch.Tensor, gate: torch.Tensor, up: torch.Tensor, h: torch.Tensor, K: int, M: int) -> None:
@@ -432,5 +440,19 @@ def batched_int4_matmul(x, superblocks, K: int, M: int, out=None, *, algo: int =
         _gemm_into(xs[r0:r1], blob, y[r0:r1], K, M, algo, splits, batch, finish, front, group, waves, tile_order)
     if out is not None and not D.is_tensor(out):
         np.copyto(out, D.to_host(y))
+        D.workspaces.check("batched_int4_matmul")
         return out
-    return D.out_like(y, want_t)
+    if not want_t:  # the host copy waits for the call anyway
+        res = D.to_host(y)
+        D.workspaces.check("batched_int4_matmul")
+        return res
+    return y
+
+
+def check_gemm_workspace() -> None:
+    """Raise RuntimeError if an in-kernel hand-off of a GEMM on the current
+    stream ran out of time since the last check (those results, and those
+    of every later call on the stream's workspace, are NaN); the workspace is
+    cleared first.  Synchronises the stream.  Calls with numpy outputs check
+    by themselves."""
+    D.workspaces.check("GEMM")

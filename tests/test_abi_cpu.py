@@ -290,3 +290,30 @@ def test_tile_order_python_checks_first():
     from moat_amd import dequant
     with pytest.raises(ValueError):
         dequant.records_to_tiles(np.zeros(21 * 144, np.uint8), 1, 5376 - 128)
+
+
+def test_gemm_unaligned_x_is_validated_against_its_own_plan(lib):
+    """x only 2-byte aligned on a record-stream shape: the call plans the
+    general kernel (the record-stream kernel reads X 16 bytes at a time) and
+    checks the workspace against that plan; the size query covers both."""
+    odd_x = ctypes.c_void_p(0x10002)
+    for n in (1, 8):
+        general = _lib.GemmOptions(0, 0, 0, 0, _lib.FRONT_LDS)
+        g_size = lib.moat_int4_gemm_ex_workspace_size(n, 2048, 5504, ctypes.byref(general))
+        a_size = lib.moat_int4_gemm_workspace_size(n, 2048, 5504)
+        assert g_size > 0 and a_size >= g_size
+        st = lib.moat_int4_gemm(odd_x, FAKE, FAKE, n, 2048, 5504, FAKE, g_size - 1, None)
+        assert st == _lib.MOAT_ERR_WORKSPACE
+        # the same explicit record-stream request also falls back to the general plan
+        rec = _lib.GemmOptions(0, 0, 0, 0, _lib.FRONT_RECORDS)
+        st = lib.moat_int4_gemm_ex(odd_x, FAKE, FAKE, n, 2048, 5504, ctypes.byref(rec), FAKE, g_size - 1, None)
+        assert st == _lib.MOAT_ERR_WORKSPACE
+    # tile order has no general kernel: refused outright
+    assert lib.moat_int4_gemm_tiles(odd_x, FAKE, FAKE, 1, 2048, 8192, None, FAKE, 1 << 30, None) == _lib.MOAT_ERR_INVALID
+
+
+def test_workspace_status_rejects_bad_arguments(lib):
+    st = ctypes.c_int32(0)
+    assert lib.moat_int4_workspace_status(None, 1 << 20, ctypes.byref(st), None) == _lib.MOAT_ERR_INVALID
+    assert lib.moat_int4_workspace_status(FAKE, 255, ctypes.byref(st), None) == _lib.MOAT_ERR_INVALID
+    assert lib.moat_int4_workspace_status(FAKE, 1 << 20, None, None) == _lib.MOAT_ERR_INVALID

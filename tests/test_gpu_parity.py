@@ -221,6 +221,60 @@ def test_gemm_equals_stacked_gemv():
         assert rel_err(y, rows) <= TOL
 
 
+@pytest.mark.parametrize("seed,ns", [(42, [8]), (7, [1, 2, 4, 8, 16])])
+def test_gemm_equals_sequential_gemvs_2048(seed, ns):
+    """The reference's must-pass invariant at its own shape, K = M = 2048
+    (antigravity-engine/tests/test_batched_speed.py:55-86): W and the
+    activations drawn as there (np.random.seed, randn as fp16), W quantized
+    to superblocks; GEMM(N) equals N sequential N=1 calls and the oracle."""
+    from moat_amd.dequant import batched_int4_matmul
+    K = M = 2048
+    np.random.seed(seed)
+    w = np.random.randn(K, M).astype(np.float16)
+    blob = O.quantize_pack_a(w)
+    wdq = O.decode_superblocks(blob, K * M // 256).astype(np.float32).reshape(K, M)
+    blob_d = torch.from_numpy(blob.reshape(-1)).cuda()
+    for N in ns:
+        acts = np.random.randn(N, K).astype(np.float16)
+        xd = torch.from_numpy(acts).cuda()
+        say(f"case: 2048x2048 seed={seed} N={N}: GEMM vs {N} sequential GEMVs")
+        y = batched_int4_matmul(xd, blob_d, K, M).cpu().numpy()
+        seq = np.vstack([batched_int4_matmul(xd[i:i + 1], blob_d, K, M).cpu().numpy() for i in range(N)])
+        yref = acts.astype(np.float32) @ wdq
+        assert rel_err(y, seq) <= TOL
+        assert rel_err(y, yref) <= TOL and rel_err(seq, yref) <= TOL
+        assert np.all(np.isfinite(y))
+
+
+def test_gemm_unaligned_x_on_record_stream_shape_through_abi():
+    """x only 2-byte aligned on a shape the record-stream kernel takes: the
+    call plans the general kernel, and the workspace the size query gives
+    covers that plan (called through the C ABI, no Python re-alignment)."""
+    import ctypes
+    L = _lib()
+    lib = L.load()
+    K, M, _, blob = workload("ffn 2048x5504")
+    wdq = O.decode_superblocks(blob, K * M // 256).astype(np.float32).reshape(K, M)
+    blob_d = torch.from_numpy(blob.reshape(-1)).cuda()
+    for N in (1, 8, 32):
+        x = _x(N, K, 600 + N)
+        yref = x.astype(np.float32) @ wdq
+        base = torch.zeros(N * K + 8, dtype=torch.float16, device="cuda")
+        xv = base[1:1 + N * K]
+        xv.copy_(torch.from_numpy(x.reshape(-1)).cuda())
+        assert xv.data_ptr() % 16 == 2
+        y = torch.full((N, M), float("nan"), dtype=torch.float32, device="cuda")
+        for opt in (None, L.GemmOptions(0, 0, 0, 0, L.FRONT_RECORDS)):
+            ref = ctypes.byref(opt) if opt is not None else None
+            ws_bytes = lib.moat_int4_gemm_ex_workspace_size(N, K, M, ref)
+            ws = torch.zeros(max(ws_bytes, 1), dtype=torch.uint8, device="cuda")
+            say(f"case: unaligned x through the ABI N={N} options={'front records' if opt else 'auto'}")
+            st = lib.moat_int4_gemm_ex(xv.data_ptr(), blob_d.data_ptr(), y.data_ptr(), N, K, M, ref,
+                                       ws.data_ptr(), ws_bytes, torch.cuda.current_stream().cuda_stream)
+            assert st == 0
+            assert rel_err(y.cpu().numpy(), yref) <= TOL
+
+
 def test_gemm_runner_stream_closed_form():
     """antigravity-engine/src/metal_runner.cpp:84-98: every output is -0.5*K, exactly."""
     from moat_amd.dequant import batched_int4_matmul
