@@ -41,6 +41,7 @@ extern "C" {
 #define MOAT_ERR_INVALID (-2)     /* bad shape, size, pointer or alignment */
 #define MOAT_ERR_HIP (-3)         /* a HIP runtime call or kernel launch failed */
 #define MOAT_ERR_WORKSPACE (-4)   /* workspace missing or too small */
+#define MOAT_ERR_TOO_LARGE (-5)   /* moat_int4_gemm_noalloc: the plan needs more scratch than it holds */
 
 /* element types for the typed entry points */
 #define MOAT_DTYPE_F32 0
@@ -105,6 +106,23 @@ int64_t moat_int4_gemm_workspace_size(int32_t n, int32_t k, int32_t m);
 int32_t moat_int4_gemm(const uint16_t* x_f16, const uint8_t* superblocks, float* y_f32,
                        int32_t n, int32_t k, int32_t m,
                        void* workspace, int64_t workspace_bytes, hipStream_t stream);
+
+/*
+ * moat_int4_gemm without a workspace: the same product, plan and kernels,
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  No
+ * counterpart in the reference.  Split-K partials go to a 16 MB scratch
+ * array inside the library, one per GPU, held until the process ends (its
+ * address is looked up on the first call on each device); they are always
+ * summed by the fix-up kernel, so nothing in the scratch must start at zero.
+ * A call whose plan needs more than 16 MB (the general kernel's plan for
+ * very wide outputs) returns MOAT_ERR_TOO_LARGE; use moat_int4_gemm with a
+ * workspace instead.  Calls on one GPU share that scratch: calls that overlap
+ * in time on one GPU (different streams, concurrent graphs) race and must
+ * not be issued; calls in order on one stream are fine.  Allocates nothing.
+ */
+int32_t moat_int4_gemm_noalloc(const uint16_t* x_f16, const uint8_t* superblocks, float* y_f32,
+                               int32_t n, int32_t k, int32_t m, hipStream_t stream);
 
 /* Launch choices for moat_int4_gemm_ex; zero-initialise for "automatic". */
 typedef struct moat_int4_gemm_options {

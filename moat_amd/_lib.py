@@ -19,6 +19,7 @@ MOAT_OK = 0
 MOAT_ERR_INVALID = -2
 MOAT_ERR_HIP = -3
 MOAT_ERR_WORKSPACE = -4
+MOAT_ERR_TOO_LARGE = -5
 WS_HANDOFF_TIMEOUT = 1
 
 DTYPE_F32, DTYPE_F16, DTYPE_I8, DTYPE_F64, DTYPE_I64 = 0, 1, 2, 3, 4
@@ -46,6 +47,7 @@ SIGNATURES = {
     "moat_int4_dequant": (_I32, [_P, _I64, _P, _P]),
     "moat_int4_gemm_workspace_size": (_I64, [_I32, _I32, _I32]),
     "moat_int4_gemm": (_I32, [_P, _P, _P, _I32, _I32, _I32, _P, _I64, _P]),
+    "moat_int4_gemm_noalloc": (_I32, [_P, _P, _P, _I32, _I32, _I32, _P]),
     "moat_int4_gemm_ex_workspace_size": (_I64, [_I32, _I32, _I32, ctypes.POINTER(GemmOptions)]),
     "moat_int4_gemm_ex": (_I32, [_P, _P, _P, _I32, _I32, _I32, ctypes.POINTER(GemmOptions), _P, _I64, _P]),
     "moat_int4_records_to_tiles": (_I32, [_P, _I32, _I32, _P, _P]),
@@ -102,6 +104,6 @@ def check(status: int, what: str) -> None:
     if status == MOAT_OK:
         return
     msg = load().moat_int4_status_string(status).decode()
-    if status in (MOAT_ERR_INVALID, MOAT_ERR_WORKSPACE):
+    if status in (MOAT_ERR_INVALID, MOAT_ERR_WORKSPACE, MOAT_ERR_TOO_LARGE):
         raise ValueError(f"{what}: {msg} (status {status})")
     raise RuntimeError(f"{what}: {msg} (status {status})")

@@ -2,6 +2,9 @@
 // planning of the GEMM launch, and dispatch to the kernels.
 #include <stdint.h>
 
+#include <atomic>
+#include <mutex>
+
 #include <hip/hip_runtime.h>
 
 #include "../../include/moat_int4.h"
@@ -307,15 +310,68 @@ bool sample_ws_ok(int32_t n, int32_t v, bool with_e, const void* workspace, int6
 }
 
 
-// The GEMM over records in row order (tile_order 0) or tile order (1).
+// Scratch of moat_int4_gemm_noalloc: one static device array, which every
+// GPU the library runs on holds (its own copy, at its own address) until the
+// process ends.  Its address on a device comes from hipGetSymbolAddress with
+// that device current, once per device; host code uses only that address (the
+// array's name in host code is a host-side stand-in, not device memory).
+// Calls that use it always hand split-K partials to the fix-up kernel, which
+// needs nothing to start at zero: whatever an earlier call left there is
+// overwritten before it is read.
+constexpr int64_t kNoallocScratchBytes = 16 << 20;
+
+}  // namespace
+
+static __device__ __align__(256) uint8_t scratch[kNoallocScratchBytes];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// The scratch address on the current device (looked up on its first use).
+int32_t noalloc_scratch(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess) return MOAT_ERR_HIP;
+  if (dev < 0 || dev >= kMaxDevices) return MOAT_ERR_INVALID;
+  void* ptr = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!ptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    ptr = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (!ptr) {
+      size_t bytes = 0;
+      if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return MOAT_ERR_HIP;
+      if (hipGetSymbolSize(&bytes, HIP_SYMBOL(scratch)) != hipSuccess || bytes < (size_t)kNoallocScratchBytes)
+        return MOAT_ERR_HIP;
+      g_scratch_ptr[dev].store(ptr, std::memory_order_release);
+    }
+  }
+  *out = ptr;
+  return MOAT_OK;
+}
+
+// The GEMM over records in row order (tile_order 0) or tile order (1).  With
+// `noalloc`, the workspace is the library's own scratch: any split-K plan
+// hands its partials to the fix-up kernel (no in-kernel hand-off, so no
+// status word and nothing that must start at zero), and a plan needing more
+// than the scratch holds is refused.
 int32_t gemm_call(const uint16_t* x_f16, const uint8_t* superblocks, float* y_f32, int32_t n, int32_t k, int32_t m,
                   const moat_int4_gemm_options* options, void* workspace, int64_t workspace_bytes, int tile_order,
-                  hipStream_t stream) {
+                  hipStream_t stream, bool noalloc = false) {
   if (!gemm_shape_ok(n, k, m) || !options_ok(options, n)) return MOAT_ERR_INVALID;
   if (!x_f16 || !superblocks || !y_f32) return MOAT_ERR_INVALID;
   if (!aligned(x_f16, 2) || !aligned(superblocks, 16) || !aligned(y_f32, 4)) return MOAT_ERR_INVALID;
   const bool x_vec = aligned(x_f16, 16) && (k % 8) == 0;
   const GemmPlan p = plan_gemm(n, k, m, options, x_vec);
+  if (noalloc) {
+    if (p.workspace_bytes > kNoallocScratchBytes) return MOAT_ERR_TOO_LARGE;
+    if (p.workspace_bytes > 0) {
+      const int32_t st = noalloc_scratch(&workspace);
+      if (st != MOAT_OK) return st;
+      workspace_bytes = kNoallocScratchBytes;
+    }
+  }
   if (p.algo == MOAT_GEMM_DOT2 && n > kMaxDot2N) return MOAT_ERR_INVALID;
   // tile order: the record-stream kernel only (whole 256-column tiles, whole
   // 32-row rounds, 16-byte X rows)
@@ -326,7 +382,7 @@ int32_t gemm_call(const uint16_t* x_f16, const uint8_t* superblocks, float* y_f3
   uint32_t* status = nullptr;
   if (p.workspace_bytes > 0) {
     if (!workspace || workspace_bytes < p.workspace_bytes || !aligned(workspace, 16)) return MOAT_ERR_WORKSPACE;
-    status = static_cast<uint32_t*>(workspace);
+    status = noalloc ? nullptr : static_cast<uint32_t*>(workspace);
     counters = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(workspace) + moat::kWsStatusBytes);
     partials = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + p.counter_bytes);
   }
@@ -349,6 +405,7 @@ const char* moat_int4_status_string(int32_t status) {
     case MOAT_ERR_INVALID: return "invalid argument (shape, size, pointer or alignment)";
     case MOAT_ERR_HIP: return "HIP runtime error";
     case MOAT_ERR_WORKSPACE: return "workspace missing or too small";
+    case MOAT_ERR_TOO_LARGE: return "the call needs more split-K scratch than moat_int4_gemm_noalloc holds (16 MB)";
     default: return "unknown status";
   }
 }
@@ -399,6 +456,12 @@ int32_t moat_int4_records_to_tiles(const uint8_t* superblocks, int32_t k, int32_
 int32_t moat_int4_gemm(const uint16_t* x_f16, const uint8_t* superblocks, float* y_f32, int32_t n, int32_t k,
                        int32_t m, void* workspace, int64_t workspace_bytes, hipStream_t stream) {
   return moat_int4_gemm_ex(x_f16, superblocks, y_f32, n, k, m, nullptr, workspace, workspace_bytes, stream);
+}
+
+int32_t moat_int4_gemm_noalloc(const uint16_t* x_f16, const uint8_t* superblocks, float* y_f32, int32_t n, int32_t k,
+                               int32_t m, hipStream_t stream) {
+  const moat_int4_gemm_options opt = {0, 0, 0, MOAT_FINISH_SECOND_KERNEL, 0, 0, 0};
+  return gemm_call(x_f16, superblocks, y_f32, n, k, m, &opt, nullptr, 0, 0, stream, true);
 }
 
 int64_t moat_int4_gemm_multi_workspace_size(int32_t count, int32_t n, int32_t k, int32_t m) {

@@ -317,3 +317,16 @@ def test_workspace_status_rejects_bad_arguments(lib):
     assert lib.moat_int4_workspace_status(None, 1 << 20, ctypes.byref(st), None) == _lib.MOAT_ERR_INVALID
     assert lib.moat_int4_workspace_status(FAKE, 255, ctypes.byref(st), None) == _lib.MOAT_ERR_INVALID
     assert lib.moat_int4_workspace_status(FAKE, 1 << 20, None, None) == _lib.MOAT_ERR_INVALID
+
+
+def test_gemm_noalloc_validates_before_any_hip_call(lib):
+    assert lib.moat_int4_gemm_noalloc(FAKE, FAKE, FAKE, 0, 256, 256, None) == _lib.MOAT_ERR_INVALID
+    assert lib.moat_int4_gemm_noalloc(None, FAKE, FAKE, 1, 256, 256, None) == _lib.MOAT_ERR_INVALID
+    assert lib.moat_int4_gemm_noalloc(FAKE, ctypes.c_void_p(0x10008), FAKE, 1, 256, 256, None) == _lib.MOAT_ERR_INVALID
+    # 32 rows over 128 tile groups: 256 workgroups with 32 KB of partials
+    # each, more than the 16 MB scratch: refused with its own status
+    size = lib.moat_int4_gemm_ex_workspace_size(32, 8192, 32768, ctypes.byref(_lib.GemmOptions(0, 0, 0, 3)))
+    assert size > 16 << 20
+    st = lib.moat_int4_gemm_noalloc(FAKE, FAKE, FAKE, 32, 8192, 32768, None)
+    assert st == _lib.MOAT_ERR_TOO_LARGE
+    assert b"16 MB" in lib.moat_int4_status_string(st)
