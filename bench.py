@@ -233,11 +233,11 @@ class Timer:
         return self.replay_us([g], reps) / (reps * calls)
 
 
-def build_projection(torch, dev, config, tile_order):
-    """Weights of `config` quantized on the GPU (row order, or tile order),
+def build_projection(torch, dev, config, layout):
+    """Weights of `config` quantized on the GPU (row, tile or strip order),
     and enough copies of the records that the rotated set exceeds the 256 MB
     Infinity Cache."""
-    from moat_amd.dequant import quantize_to_superblocks, records_to_tiles
+    from moat_amd.dequant import quantize_to_superblocks, records_to_strips, records_to_tiles
     K, M, std, seed, outl, _ = CONFIGS[config]
     rng = np.random.default_rng(seed)
     w = rng.standard_normal((K, M), dtype=np.float32) * np.float32(std)
@@ -248,24 +248,26 @@ def build_projection(torch, dev, config, tile_order):
     blob0 = quantize_to_superblocks(torch.from_numpy(w).to(dev))  # (S, 144) uint8 on the GPU
     del w
     row_blob = blob0
-    if tile_order:
+    if layout == "tile":
         blob0 = records_to_tiles(blob0, K, M)
+    elif layout == "strip":
+        blob0 = records_to_strips(blob0, K, M)
     copies = max(2, -(-ROTATE_BYTES // blob0.numel()))
     blobs = [blob0] + [blob0.clone() for _ in range(copies - 1)]
     return blobs, row_blob
 
 
-def measure_projection(torch, timer, lib, config, ns, tile_order, args, with_floor=True):
+def measure_projection(torch, timer, lib, config, ns, layout, args, with_floor=True):
     """Per-N figures of one projection shape: per-call time (graph replay),
     kernel time (events around each call), the streaming-read floor of the
     same record bytes, GB/s and roofline fraction on the kernel time."""
     from moat_amd.dequant import _gemm_into
     dev = torch.device("cuda", 0)
     K, M = CONFIGS[config][:2]
-    blobs, row_blob = build_projection(torch, dev, config, tile_order)
+    blobs, row_blob = build_projection(torch, dev, config, layout)
     copies = len(blobs)
     sb_bytes = blobs[0].numel()
-    order = "tile" if tile_order else "row"
+    order = layout
     log(f"[bench] {config} ({order} order): K={K} M={M}, {copies} copies of {sb_bytes / 1e6:.2f} MB records")
     xs = {N: torch.from_numpy(np.random.default_rng(2000 + 100 * 2 + N).standard_normal((N, K), dtype=np.float32)
                               .astype(np.float16)).to(dev) for N in ns}
@@ -273,7 +275,7 @@ def measure_projection(torch, timer, lib, config, ns, tile_order, args, with_flo
 
     def call(N, i):
         _gemm_into(xs[N], blobs[i % copies], ys[N], K, M, args.algo, args.splits, args.batch, args.finish,
-                   args.front, tile_order=tile_order)
+                   args.front, waves=args.waves, tile_order=layout == "tile", strip_order=layout == "strip")
 
     with torch.cuda.stream(timer.cap):
         for N in ns:  # creates this stream's workspace before any capture
@@ -337,11 +339,15 @@ def main() -> int:
                     help="skip the K=8192 x M=28672 block measured beside the default workload")
     ap.add_argument("--batch", type=int, default=0, help="rounds of loads issued together (0 auto)")
     ap.add_argument("--finish", type=int, default=0, help="split-K hand-off (0 auto, 1 atomics, 2 fences, 3 kernel)")
+    ap.add_argument("--waves", type=int, default=0, help="waves per workgroup, 4 or 8 (0 auto)")
     ap.add_argument("--front", type=int, default=0,
                     help="load front end (0 auto, 1 LDS-staged, 2 direct, 3 LDS DMA, 4 record stream)")
     ap.add_argument("--tile-order", action="store_true",
                     help="GEMM configs: weights stored in tile order (each 256-column tile's rows contiguous; "
                          "moat_int4_records_to_tiles), read by moat_int4_gemm_tiles; needs M %% 256 == 0")
+    ap.add_argument("--strip-order", action="store_true",
+                    help="GEMM configs: weights stored in strip order (moat_int4_records_to_strips), read by "
+                         "moat_int4_gemm_strips; needs K >= 2048")
     ap.add_argument("--fused", action="store_true",
                     help="layer_h2048: Q, K, V in one launch and gate/up fused with SwiGLU (h feeds down)")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"), default=None,
@@ -384,7 +390,8 @@ def main() -> int:
         return 2
     ns = [int(v) for v in args.ns.split(",")] if args.ns else CONFIGS[args.config][5]
     timer = Timer(torch)
-    main_res = measure_projection(torch, timer, lib, args.config, ns, args.tile_order, args)
+    layout = "strip" if args.strip_order else ("tile" if args.tile_order else "row")
+    main_res = measure_projection(torch, timer, lib, args.config, ns, layout, args)
     per_n, call = main_res["per_n"], main_res["call"]
     copies = main_res["copies"]
 
@@ -408,9 +415,9 @@ def main() -> int:
     if args.config == DEFAULT_CONFIG and not args.no_side and not args.ns:
         side_cfg, side_ns = SIDE_CONFIG
         side = {}
-        for tile in (True, False):
-            r = measure_projection(torch, timer, lib, side_cfg, side_ns, tile, args, with_floor=tile)
-            side["tile_order" if tile else "row_order"] = {
+        for lay in ("strip", "tile", "row"):
+            r = measure_projection(torch, timer, lib, side_cfg, side_ns, lay, args, with_floor=lay == "strip")
+            side[lay + "_order"] = {
                 "per_n": {str(k): v for k, v in r["per_n"].items()}, "read_floor": r["read_floor"],
                 "copies": r["copies"]}
             del r
@@ -432,7 +439,7 @@ def main() -> int:
     }
     traffic_file = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                                 f"traffic_{args.config}.json")
-    if os.path.exists(traffic_file) and not args.tile_order:
+    if os.path.exists(traffic_file) and layout == "row":
         with open(traffic_file) as f:
             tr = json.load(f).get(str(dom))
         if tr is not None:
@@ -467,7 +474,7 @@ def main() -> int:
                              "HIP events on the launch stream",
                    "algo": args.algo, "splits": args.splits, "batch": args.batch, "finish": args.finish,
                    "front": args.front, "weights": "int4 superblocks (144 B per 256 weights)"
-                   + (", tile order" if args.tile_order else ", row order"),
+                   + f", {layout} order",
                    "activations": "fp16", "output": "fp32"},
         "per_n": {str(k): v for k, v in per_n.items()},
         "read_floor": main_res["read_floor"],

@@ -191,6 +191,37 @@ int32_t moat_int4_gemm_tiles(const uint16_t* x_f16, const uint8_t* tiles, float*
                              int32_t n, int32_t k, int32_t m, const moat_int4_gemm_options* options,
                              void* workspace, int64_t workspace_bytes, hipStream_t stream);
 
+/*
+ * Strip order: a storage order for the same quantized weights that a loader
+ * chooses once (no counterpart in the reference, whose stream is the row
+ * order of src/dequant.py:116-147).  Strip g = columns 32g .. 32g+31 of W;
+ * strips follow each other in column order, and inside strip g record b
+ * (144 bytes) holds rows 8b .. 8b+7: bytes [0,16) the 8 fp16 scales of those
+ * rows' group g, bytes [16 + 16i, 32 + 16i) row 8b+i's 16 payload bytes of
+ * group g, in the record format's nibble order.  The q values and scales are
+ * those of the row-order stream, bit for bit; a strip is one contiguous run
+ * of K x 18 bytes, and the GEMM's workgroups each stream one contiguous
+ * range of them.
+ *
+ * moat_int4_records_to_strips: row order -> strip order (k % 8 == 0,
+ * m % 32 == 0; both 16-byte aligned, not overlapping).
+ * moat_int4_gemm_strips: Y = X @ deq(W) over a strip-order stream, the same
+ * product and tolerance as moat_int4_gemm.  Preconditions: 1 <= n <= 32,
+ * k >= 2048, k % 32 == 0, m % 32 == 0; x 16-byte aligned, strips 16-byte
+ * aligned, y 4-byte aligned (MOAT_ERR_INVALID otherwise).  Rows of X are
+ * taken 8 per launch.  Workspace as for moat_int4_gemm (zeroed once, left
+ * zero, shares the status word), sized by
+ * moat_int4_gemm_strips_workspace_size; options: `splits` = workgroups
+ * (0 automatic), `batch` = ring depth (0 automatic), the rest ignored.
+ */
+int32_t moat_int4_records_to_strips(const uint8_t* superblocks, int32_t k, int32_t m, uint8_t* strips,
+                                    hipStream_t stream);
+int64_t moat_int4_gemm_strips_workspace_size(int32_t n, int32_t k, int32_t m,
+                                             const moat_int4_gemm_options* options);
+int32_t moat_int4_gemm_strips(const uint16_t* x_f16, const uint8_t* strips, float* y_f32,
+                              int32_t n, int32_t k, int32_t m, const moat_int4_gemm_options* options,
+                              void* workspace, int64_t workspace_bytes, hipStream_t stream);
+
 /* Zero `bytes` bytes of device memory with a kernel (no memset node). */
 int32_t moat_int4_workspace_clear(void* workspace, int64_t bytes, hipStream_t stream);
 

@@ -53,6 +53,9 @@ SIGNATURES = {
     "moat_int4_records_to_tiles": (_I32, [_P, _I32, _I32, _P, _P]),
     "moat_int4_gemm_tiles": (_I32, [_P, _P, _P, _I32, _I32, _I32, ctypes.POINTER(GemmOptions), _P, _I64, _P]),
     "moat_int4_workspace_clear": (_I32, [_P, _I64, _P]),
+    "moat_int4_records_to_strips": (_I32, [_P, _I32, _I32, _P, _P]),
+    "moat_int4_gemm_strips_workspace_size": (_I64, [_I32, _I32, _I32, ctypes.POINTER(GemmOptions)]),
+    "moat_int4_gemm_strips": (_I32, [_P, _P, _P, _I32, _I32, _I32, ctypes.POINTER(GemmOptions), _P, _I64, _P]),
     "moat_int4_workspace_status": (_I32, [_P, _I64, ctypes.POINTER(_I32), _P]),
     "moat_int4_stream_read": (_I32, [_P, _I64, _I32, _P, _P]),
     "moat_int4_gemm_multi_workspace_size": (_I64, [_I32, _I32, _I32, _I32]),

@@ -49,6 +49,11 @@ hipError_t launch_gemm(int algo, const uint16_t* x, const uint8_t* sb, float* y,
                        uint32_t* counters, uint32_t* status, int tile_order, hipStream_t stream);
 hipError_t launch_records_to_tiles(const uint8_t* sb, int k, int m, uint8_t* tiles, hipStream_t stream);
 hipError_t launch_stream_read(const void* src, int64_t bytes, uint32_t* sink, int blocks, hipStream_t st);
+hipError_t launch_gemm_strips(const uint16_t* x, const uint8_t* w, float* y, int n, int k, int m, int wgs, int depth,
+                              int waves, float* slots, uint32_t* status, hipStream_t stream);
+hipError_t launch_records_to_strips(const uint8_t* sb, int k, int m, uint8_t* strips, hipStream_t stream);
+int strips_waves(int n, int waves);
+int strips_depth(int n, int waves, int depth);
 }  // namespace moat
 
 namespace {
@@ -391,6 +396,57 @@ int32_t gemm_call(const uint16_t* x_f16, const uint8_t* superblocks, float* y_f3
 }
 
 
+// ---- strip order
+
+// Rows of X one strip-kernel launch takes; more rows run as several launches.
+constexpr int kStripRowsPerLaunch = 8;
+// At most one workgroup per CU (the kernel's LDS allows no second): all of a
+// launch's workgroups are resident together, so a strip's owner never waits
+// for a workgroup that cannot start.
+constexpr int64_t kStripMaxWorkgroups = 256;
+
+// K % 32 == 0 with at least 64 units of 32 rows per strip (K >= 2048: a
+// wave's stage then meets at most one strip boundary), M % 32 == 0.
+bool strips_shape_ok(int32_t n, int32_t k, int32_t m) {
+  if (n < 1 || n > kMaxN || k < 2048 || (k % 32) != 0 || m < 32 || (m % 32) != 0) return false;
+  if ((int64_t)(m / 32) * (k / 32) > ((int64_t)1 << 30)) return false;  // unit indices are 32-bit
+  if ((int64_t)kStripRowsPerLaunch * k * 2 > ((int64_t)1 << 31)) return false;  // X offsets are 32-bit
+  return true;
+}
+
+struct StripPlan {
+  int wgs;
+  int depth;
+  int waves;
+  int64_t workspace_bytes;
+};
+
+bool strip_options_ok(const moat_int4_gemm_options* o) {
+  return !o || (o->splits >= 0 && o->batch >= 0 && (o->waves == 0 || o->waves == 4 || o->waves == 8));
+}
+
+// Workgroups: one whole strip each when M/32 is 128..256 (nothing shared);
+// otherwise up to 256 (one per CU: the kernel's LDS leaves room for one),
+// at least 16 units each.  Shared strips need the status word and one slot
+// of 8 x 32 floats per workgroup, after the fixed 64 KB block.
+StripPlan plan_strips(int32_t n, int32_t k, int32_t m, const moat_int4_gemm_options* o) {
+  StripPlan p;
+  const int64_t strips = m / 32, units = k / 32, total = strips * units;
+  int64_t wgs;
+  if (o && o->splits > 0) wgs = o->splits < kStripMaxWorkgroups ? o->splits : kStripMaxWorkgroups;
+  else if (strips >= 128 && strips <= 256) wgs = strips;
+  else wgs = total / 16 < 256 ? (total / 16 > 0 ? total / 16 : 1) : 256;
+  if (wgs > total) wgs = total;
+  p.wgs = (int)wgs;
+  const int rows = n < kStripRowsPerLaunch ? n : kStripRowsPerLaunch;
+  p.waves = moat::strips_waves(rows, o ? o->waves : 0);
+  p.depth = moat::strips_depth(rows, p.waves, o ? o->batch : 0);
+  const int64_t base = total / wgs, rem = total % wgs;
+  const bool shared = !(rem == 0 && base % units == 0);
+  p.workspace_bytes = shared ? kCounterBlockBytes + wgs * kStripRowsPerLaunch * 32 * (int64_t)sizeof(float) : 0;
+  return p;
+}
+
 int sample_dtype(int32_t dtype) { return dtype == MOAT_DTYPE_F32 ? 0 : dtype == MOAT_DTYPE_F16 ? 1 : 2; }
 
 }  // namespace
@@ -440,6 +496,47 @@ int32_t moat_int4_gemm_tiles(const uint16_t* x_f16, const uint8_t* tiles, float*
                              int32_t m, const moat_int4_gemm_options* options, void* workspace,
                              int64_t workspace_bytes, hipStream_t stream) {
   return gemm_call(x_f16, tiles, y_f32, n, k, m, options, workspace, workspace_bytes, 1, stream);
+}
+
+int32_t moat_int4_records_to_strips(const uint8_t* superblocks, int32_t k, int32_t m, uint8_t* strips,
+                                    hipStream_t stream) {
+  if (k < 8 || (k % 8) != 0 || m < 32 || (m % 32) != 0) return MOAT_ERR_INVALID;
+  if ((int64_t)k * (m / 32) > ((int64_t)1 << 40)) return MOAT_ERR_INVALID;
+  if (!superblocks || !strips || !aligned(superblocks, 16) || !aligned(strips, 16)) return MOAT_ERR_INVALID;
+  const int64_t bytes = (int64_t)k * m / 256 * 144;
+  const uintptr_t a = reinterpret_cast<uintptr_t>(superblocks), b = reinterpret_cast<uintptr_t>(strips);
+  if (a < b + (uintptr_t)bytes && b < a + (uintptr_t)bytes) return MOAT_ERR_INVALID;  // the copies overlap
+  return status_of(moat::launch_records_to_strips(superblocks, k, m, strips, stream));
+}
+
+int64_t moat_int4_gemm_strips_workspace_size(int32_t n, int32_t k, int32_t m,
+                                             const moat_int4_gemm_options* options) {
+  if (!strips_shape_ok(n, k, m) || !strip_options_ok(options)) return -1;
+  return plan_strips(n, k, m, options).workspace_bytes;
+}
+
+int32_t moat_int4_gemm_strips(const uint16_t* x_f16, const uint8_t* strips, float* y_f32, int32_t n, int32_t k,
+                              int32_t m, const moat_int4_gemm_options* options, void* workspace,
+                              int64_t workspace_bytes, hipStream_t stream) {
+  if (!strips_shape_ok(n, k, m) || !strip_options_ok(options)) return MOAT_ERR_INVALID;
+  if (!x_f16 || !strips || !y_f32 || !aligned(x_f16, 16) || !aligned(strips, 16) || !aligned(y_f32, 4))
+    return MOAT_ERR_INVALID;
+  const StripPlan p = plan_strips(n, k, m, options);
+  float* slots = nullptr;
+  uint32_t* status = nullptr;
+  if (p.workspace_bytes > 0) {
+    if (!workspace || workspace_bytes < p.workspace_bytes || !aligned(workspace, 16)) return MOAT_ERR_WORKSPACE;
+    status = static_cast<uint32_t*>(workspace);
+    slots = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + kCounterBlockBytes);
+  }
+  // 8 rows of X per launch; the launches share the workspace in stream order
+  for (int32_t r0 = 0; r0 < n; r0 += kStripRowsPerLaunch) {
+    const int32_t rows = n - r0 < kStripRowsPerLaunch ? n - r0 : kStripRowsPerLaunch;
+    const hipError_t e = moat::launch_gemm_strips(x_f16 + (int64_t)r0 * k, strips, y_f32 + (int64_t)r0 * m, rows,
+                                                  k, m, p.wgs, p.depth, p.waves, slots, status, stream);
+    if (e != hipSuccess) return MOAT_ERR_HIP;
+  }
+  return MOAT_OK;
 }
 
 int32_t moat_int4_records_to_tiles(const uint8_t* superblocks, int32_t k, int32_t m, uint8_t* tiles,

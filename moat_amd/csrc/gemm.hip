@@ -56,8 +56,7 @@
 //    to the 8 XCDs) works on one contiguous range of (split, tile) pairs:
 //    neighbouring column tiles share 128-byte lines, which then meet in the
 //    same L2.
-#include "handoff.h"
-#include "superblock_device.h"
+#include "stream_device.h"
 
 namespace moat {
 
@@ -206,7 +205,6 @@ __device__ __forceinline__ void direct_round(RoundData& d, const DirectOffsets& 
 constexpr int kStagePayload = 2048;               // 32 rows x 4 group chunks x 16 B
 constexpr int kStageRound = kStagePayload + 256;  // + 32 rows x 4 fp16 scales
 
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 // Per-lane source offsets (round 0) of its three load slots:
 //  payload slot s = 64*i + lane (i = 0, 1) holds row 8*((s>>2)&3) + (s>>4),
@@ -695,35 +693,6 @@ __device__ __forceinline__ void rec_slots(RecSlots& s, int lane, int m) {
   }
 }
 
-// s_waitcnt vmcnt(N) (gfx9 encoding; expcnt and lgkmcnt left unconstrained),
-// then a compiler barrier so that no LDS read of the stage moves above it.
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
-  asm volatile("" ::: "memory");
-}
-
-// Inline assembly that reads scalar registers in a vector memory instruction
-// starts with kSgprVmemNops: on gfx9 a VMEM instruction needs 5 wait states
-// after a VALU instruction (v_readlane, v_readfirstlane, v_cmp ...) writes an
-// SGPR it reads, and the compiler, which inserts those wait states between
-// its own instructions, does not look inside inline assembly -- it may reload
-// a spilled base address with v_readlane right before the block.
-#define MOAT_SGPR_VMEM_NOPS "s_nop 4\n\t"
-
-// One global_load_lds_dwordx4: lane l's 16 bytes at base + off (base in
-// scalar registers, a 32-bit per-lane offset) land at LDS byte lds_base +
-// 16*l.  Written as inline assembly so that the compiler, which cannot tell
-// the ring's stages apart, does not guard every later LDS read with a wait for
-// all of these copies; the explicit vmcnt waits above are the only ordering
-// the ring needs.  (s_nop 0: one wait state between writing M0 and the
-// instruction that reads it.)
-__device__ __forceinline__ void lds_dma16(const void* base, uint32_t off, uint32_t lds_base) {
-  asm volatile(MOAT_SGPR_VMEM_NOPS "s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(off),
-               "s"(base), "s"(lds_base) : "memory", "m0");
-}
-
 template <int NR>
 __device__ __forceinline__ void rec_issue(const uint32_t (&woff)[kRecWeightLoads], const uint8_t* wround,
                                           const uint8_t* xround, const uint32_t (&xoff)[NR], uint32_t stage) {
@@ -818,92 +787,6 @@ __device__ __forceinline__ int streamk_owner(const GemmParams& P, int i) {
 // of a row address 8 different 16-byte bank groups.
 __device__ __forceinline__ int red_pos(int row, int jj, int u) {
   return row * kRecCols + 16 * jj + 4 * ((u + (jj >> 2)) & 3);
-}
-
-// Device-coherent (agent scope) vector accesses for the in-kernel hand-off:
-// sc1 stores write through and sc1 loads read past the per-XCD L2s, the
-// same cache policy as relaxed agent-scope atomics, 16 bytes at a time.
-__device__ __forceinline__ void store_sc1(float* p, float4_t v) {
-  asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
-}
-
-// Partials of the in-kernel hand-off travel encoded (handoff.h): each word is
-// the bitwise complement of the value, NaN first made the canonical
-// 0x7FC00000, so a word of zero means "not written yet".  The owner of a tile
-// group clears the chunks it consumed, which leaves every slot at zero for
-// the next call.
-__device__ __forceinline__ float4_t enc_partial(float4_t v) {
-  float4_t e;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) e[i] = __uint_as_float(handoff_encode(__float_as_uint(v[i])));
-  return e;
-}
-
-__device__ __forceinline__ bool partial_ready(float4_t w) {
-  return handoff_chunk_written(__float_as_uint(w[0]), __float_as_uint(w[1]), __float_as_uint(w[2]),
-                               __float_as_uint(w[3]));
-}
-
-__device__ __forceinline__ float4_t dec_partial(float4_t w) {
-  float4_t v;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) v[i] = __uint_as_float(handoff_decode(__float_as_uint(w[i])));
-  return v;
-}
-
-// The workspace's sticky status at the start of a call, as a value to add to
-// every result: 0 when the status word is clear (or there is no workspace),
-// NaN when it is set.  Kept in a vector register (adding 0 leaves a result
-// unchanged, -0 aside), where it costs no scalar registers over the kernel.
-__device__ __forceinline__ float read_poison(const GemmParams& P) {
-  const uint32_t st = P.status ? __hip_atomic_load(P.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
-  float poison = st ? __uint_as_float(0x7FC00000u) : 0.0f;
-  asm volatile("" : "+v"(poison));
-  return poison;
-}
-
-__device__ __forceinline__ float4_t poisoned(float4_t v, float poison) {
-  return v + float4_t{poison, poison, poison, poison};
-}
-
-// Repeated batch loads a thread of the owner may spend on chunks not yet
-// written before it stops waiting and adds them as they read (NaN): about a
-// second, a bound on the wait that contributors, which store their partials
-// before they wait for anything, never let it reach.
-constexpr int kMaxPolls = 1 << 19;
-
-// Sixteen independent sc1 loads in flight, then one wait: base (scalar) +
-// per-lane 32-bit byte offsets.
-__device__ __forceinline__ void load16_sc1(float4_t (&t)[16], const float* base, const uint32_t (&o)[16]) {
-  asm volatile(
-      MOAT_SGPR_VMEM_NOPS
-      "global_load_dwordx4 %0, %16, %32 sc1\n\t"
-      "global_load_dwordx4 %1, %17, %32 sc1\n\t"
-      "global_load_dwordx4 %2, %18, %32 sc1\n\t"
-      "global_load_dwordx4 %3, %19, %32 sc1\n\t"
-      "global_load_dwordx4 %4, %20, %32 sc1\n\t"
-      "global_load_dwordx4 %5, %21, %32 sc1\n\t"
-      "global_load_dwordx4 %6, %22, %32 sc1\n\t"
-      "global_load_dwordx4 %7, %23, %32 sc1\n\t"
-      "global_load_dwordx4 %8, %24, %32 sc1\n\t"
-      "global_load_dwordx4 %9, %25, %32 sc1\n\t"
-      "global_load_dwordx4 %10, %26, %32 sc1\n\t"
-      "global_load_dwordx4 %11, %27, %32 sc1\n\t"
-      "global_load_dwordx4 %12, %28, %32 sc1\n\t"
-      "global_load_dwordx4 %13, %29, %32 sc1\n\t"
-      "global_load_dwordx4 %14, %30, %32 sc1\n\t"
-      "global_load_dwordx4 %15, %31, %32 sc1\n\t"
-      "s_waitcnt vmcnt(0)"
-      : "=&v"(t[0]), "=&v"(t[1]), "=&v"(t[2]), "=&v"(t[3]), "=&v"(t[4]), "=&v"(t[5]), "=&v"(t[6]), "=&v"(t[7]),
-        "=&v"(t[8]), "=&v"(t[9]), "=&v"(t[10]), "=&v"(t[11]), "=&v"(t[12]), "=&v"(t[13]), "=&v"(t[14]),
-        "=&v"(t[15])
-      : "v"(o[0]), "v"(o[1]), "v"(o[2]), "v"(o[3]), "v"(o[4]), "v"(o[5]), "v"(o[6]), "v"(o[7]), "v"(o[8]),
-        "v"(o[9]), "v"(o[10]), "v"(o[11]), "v"(o[12]), "v"(o[13]), "v"(o[14]), "v"(o[15]), "s"(base)
-      : "memory");
-}
-
-__device__ __forceinline__ void store_sc1_at(float* base, uint32_t o, float4_t v) {
-  asm volatile(MOAT_SGPR_VMEM_NOPS "global_store_dwordx4 %0, %1, %2 sc1" : : "v"(o), "v"(v), "s"(base) : "memory");
 }
 
 // Where a tile group's results go: tile tl of the group covers columns
@@ -1169,13 +1052,16 @@ __global__ void __launch_bounds__(kW * 64) int4_gemm_records_kernel(GemmParams P
   int lo, hi;
   streamk_range(P, p, lo, hi);
 
-  const float poison = read_poison(P);  // used only when results are written
+  // the status word's copies first in LDS, the ring and reduction slots after
+  uint32_t* lds_status = reinterpret_cast<uint32_t*>(smem);
+  uint8_t* const lds0 = smem + kStatusLdsBytes;
+  status_to_lds(P.status, lds_status);  // read once the segment's ring has drained
   const uint64_t round_bytes = P.rec_round_bytes;
   RecSlots slots;
   rec_slots(slots, lane, P.rec_row_m);
-  uint8_t* ring = smem + wave * kDepth * G::kStageBytes;
+  uint8_t* ring = lds0 + wave * kDepth * G::kStageBytes;
   const uint32_t ring_lds = (uint32_t)(uintptr_t)(lds_ptr_t)ring;  // LDS byte address (wave-uniform)
-  float* red = reinterpret_cast<float*>(smem);
+  float* red = reinterpret_cast<float*>(lds0);
   const int per_slot = P.n * kRecCols;
   constexpr int kSlots = kShare;  // reduction slots per tile: one per wave
 
@@ -1206,7 +1092,6 @@ __global__ void __launch_bounds__(kW * 64) int4_gemm_records_kernel(GemmParams P
     const uint8_t* wtile = wmat + P.rec_tile_bytes * (uint64_t)(has_tile ? ltile : 0);
     // where the group's results go (the group's first tile)
     RecOut out;
-    out.poison = poison;
     if (kMode == kModeSingle) {
       out.y = P.y;
       out.m0 = tg * kC * kRecCols;
@@ -1249,6 +1134,8 @@ __global__ void __launch_bounds__(kW * 64) int4_gemm_records_kernel(GemmParams P
       rec_compute<NR>(acc, ring + (i % kDepth) * G::kStageBytes, rd, q, smask, mw);
     }
     __syncthreads();  // the ring is reused for the reduction
+    wait_vmcnt<0>();  // the ring has drained: free
+    out.poison = status_poison(status_from_lds(lds_status));
 
     // Waves of one tile add up through LDS: each stores its accumulators in
     // its own slot of the tile, and the store below sums the slots in wave
@@ -1321,7 +1208,8 @@ __device__ __forceinline__ float4_t fixup_sum(const GemmParams& P, int group_til
 // partials in workgroup order (with SwiGLU, h from the gate and up sums).
 // One thread per 4-column quad of a tile (of a gate/up pair).
 __global__ void __launch_bounds__(256) streamk_fixup_kernel(GemmParams P, int group_tiles, int mode) {
-  const float poison = read_poison(P);
+  const float poison =
+      status_poison(P.status ? __hip_atomic_load(P.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u);
   const int per_tile = P.n * 64;
   const int tiles = mode == kModeMulti ? P.mats * P.tiles : P.tiles;  // tiles (gate/up pairs) to cover
   const int total = tiles * per_tile;
@@ -1433,16 +1321,17 @@ template <int NR, int kDepth, int kC, int kW, int kMode>
 static hipError_t launch_records_one(const GemmParams& P, int wgs, hipStream_t stream) {
   const size_t ring = (size_t)kW * kDepth * RecGeom<NR>::kStageBytes;
   const size_t red = (size_t)kC * rec_slots_per_tile(kW, kC) * P.n * kRecCols * sizeof(float);
-  if (ring > kMaxDynamicLds || red > kMaxDynamicLds) return hipErrorInvalidValue;  // never launch past the LDS
-  hipLaunchKernelGGL((int4_gemm_records_kernel<NR, kDepth, kC, kW, kMode>), dim3(wgs), dim3(kW * 64),
-                     ring > red ? ring : red, stream, P);
+  const size_t lds = (ring > red ? ring : red) + kStatusLdsBytes;
+  if (lds > kMaxDynamicLds) return hipErrorInvalidValue;  // never launch past the LDS
+  hipLaunchKernelGGL((int4_gemm_records_kernel<NR, kDepth, kC, kW, kMode>), dim3(wgs), dim3(kW * 64), lds, stream,
+                     P);
   return hipGetLastError();
 }
 
 template <int NR, int kC, int kW>
 static hipError_t launch_records_depth(const GemmParams& P, int wgs, int depth, hipStream_t stream) {
   // the ring must fit: clamp the depth (kW waves x depth stages)
-  const int max_depth = (int)(kMaxDynamicLds / ((size_t)kW * RecGeom<NR>::kStageBytes));
+  const int max_depth = (int)((kMaxDynamicLds - kStatusLdsBytes) / ((size_t)kW * RecGeom<NR>::kStageBytes));
   if (depth > max_depth) depth = max_depth;
   if (depth >= 5) return launch_records_one<NR, 5, kC, kW, kModeSingle>(P, wgs, stream);
   if (depth == 4) return launch_records_one<NR, 4, kC, kW, kModeSingle>(P, wgs, stream);

@@ -280,10 +280,18 @@ def quantize_to_superblocks(weights, scale_rule: str = "f32"):
 
 def _gemm_into(x: torch.Tensor, blob: torch.Tensor, y: torch.Tensor, K: int, M: int,
                algo: int = _lib.GEMM_AUTO, splits: int = 0, batch: int = 0, finish: int = 0, front: int = 0,
-               group: int = 0, waves: int = 0, tile_order: bool = False) -> None:
+               group: int = 0, waves: int = 0, tile_order: bool = False, strip_order: bool = False) -> None:
     lib = _lib.load()
     n = x.shape[0]
     opt = _lib.GemmOptions(algo, splits, batch, finish, front, group, waves)
+    if strip_order:
+        ws_bytes = lib.moat_int4_gemm_strips_workspace_size(n, K, M, ctypes.byref(opt))
+        if ws_bytes < 0:
+            raise ValueError(f"strip order needs K >= 2048, K % 32 == 0 and M % 32 == 0 (got K={K}, M={M}, N={n})")
+        ws = D.workspaces.get(ws_bytes)
+        _lib.check(lib.moat_int4_gemm_strips(D.ptr(x), D.ptr(blob), D.ptr(y), n, K, M, ctypes.byref(opt), D.ptr(ws),
+                                             ws_bytes, D.stream()), "batched_int4_matmul")
+        return
     ws_bytes = lib.moat_int4_gemm_ex_workspace_size(n, K, M, ctypes.byref(opt))
     if ws_bytes < 0:
         raise ValueError(f"unsupported GEMM configuration N={n} K={K} M={M} algo={algo} splits={splits} "
@@ -310,6 +318,26 @@ def records_to_tiles(superblocks, K: int, M: int) -> torch.Tensor:
     _lib.check(_lib.load().moat_int4_records_to_tiles(D.ptr(blob), K, M, D.ptr(tiles), D.stream()),
                "records_to_tiles")
     return tiles
+
+
+def records_to_strips(superblocks, K: int, M: int) -> torch.Tensor:
+    """The quantized weights of a row-major K x M stream (``K % 8 == 0``,
+    ``M % 32 == 0``) in strip order: strip g = columns 32g..32g+31, strips in
+    column order, and inside a strip one 144-byte record per 8 rows (their 8
+    scales of the strip's group, then their 8 16-byte payloads).  A GPU uint8
+    tensor, read by :func:`batched_int4_matmul` with ``strip_order=True``
+    (``K >= 2048``): every workgroup streams one contiguous range of it.  (A
+    storage order with no counterpart in the reference, whose stream is the
+    row order; the q values and scales are unchanged.)"""
+    K, M = int(K), int(M)
+    if K < 8 or K % 8 != 0 or M < 32 or M % 32 != 0:
+        raise ValueError(f"strip order needs K % 8 == 0 and M % 32 == 0 (got K={K}, M={M})")
+    n_sb = K * M // SUPERBLOCK_ELEMS
+    blob = _blob_to_device(superblocks, n_sb)
+    strips = torch.empty(n_sb * SUPERBLOCK_BYTES, dtype=torch.uint8, device=blob.device)
+    _lib.check(_lib.load().moat_int4_records_to_strips(D.ptr(blob), K, M, D.ptr(strips), D.stream()),
+               "records_to_strips")
+    return strips
 
 
 def _fused_inputs(x, K: int, M: int, blobs):
@@ -404,7 +432,7 @@ def _swiglu_into(x: torch.Tensor, gate: torch.Tensor, up: torch.Tensor, h: torch
 
 def batched_int4_matmul(x, superblocks, K: int, M: int, out=None, *, algo: int = _lib.GEMM_AUTO,
                         splits: int = 0, batch: int = 0, finish: int = 0, front: int = 0, group: int = 0,
-                        waves: int = 0, tile_order: bool = False):
+                        waves: int = 0, tile_order: bool = False, strip_order: bool = False):
     """``Y[N, M] = f32(X[N, K]) @ f32(deq(W)[K, M])`` with W the 144-byte stream
     of a row-major K x M matrix; fp32 out.  Equal (to float32 summation order)
     to decoding with :func:`unpack_superblock_weights` and a float32 matmul.
@@ -413,7 +441,9 @@ def batched_int4_matmul(x, superblocks, K: int, M: int, out=None, *, algo: int =
     ``front``/``group``/``waves`` override the launch choices of
     ``moat_int4_gemm_options`` (0 = automatic).  ``tile_order``: the stream is
     in the tile order of :func:`records_to_tiles` (``M % 256 == 0``,
-    ``K % 32 == 0``)."""
+    ``K % 32 == 0``); ``strip_order``: in the strip order of
+    :func:`records_to_strips` (``K >= 2048``, ``K % 32 == 0``; ``splits`` =
+    workgroups, ``batch`` = ring depth)."""
     want_t = D.is_tensor(x)
     K, M = int(K), int(M)
     if K < 1 or M < 32 or M % 32 != 0 or (K * M) % SUPERBLOCK_ELEMS != 0:
@@ -437,7 +467,8 @@ def batched_int4_matmul(x, superblocks, K: int, M: int, out=None, *, algo: int =
         y = torch.empty((N, M), dtype=torch.float32, device=xs.device)
     for r0 in range(0, N, MAX_BATCH_PER_CALL):
         r1 = min(N, r0 + MAX_BATCH_PER_CALL)
-        _gemm_into(xs[r0:r1], blob, y[r0:r1], K, M, algo, splits, batch, finish, front, group, waves, tile_order)
+        _gemm_into(xs[r0:r1], blob, y[r0:r1], K, M, algo, splits, batch, finish, front, group, waves, tile_order,
+                   strip_order)
     if out is not None and not D.is_tensor(out):
         np.copyto(out, D.to_host(y))
         D.workspaces.check("batched_int4_matmul")

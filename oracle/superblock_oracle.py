@@ -30,6 +30,8 @@ How each function is pinned (tests/test_oracle.py):
   runner's 0x77 stream, round trips and Python-int bit arithmetic;
 * tile order: a Python-loop index permutation on small shapes, and every
   tile's records decoding to that tile's 256 columns of W;
+* strip order: a Python-loop byte permutation on small shapes over the row
+  order's own offsets, and the strip decoder giving back W;
 * GEMM: float64 accumulation of the same products, the closed-form
   -0.5*K answer of the reference runner's synthetic stream, and
   row-by-row GEMV equality.
@@ -266,6 +268,35 @@ def records_to_tiles(blob, K: int, M: int) -> np.ndarray:
     t = M // SB_ELEMS
     rec = np.asarray(blob, dtype=np.uint8).reshape(K, t, SB_BYTES)
     return np.ascontiguousarray(rec.transpose(1, 0, 2)).reshape(-1)
+
+
+def records_to_strips(blob, K: int, M: int) -> np.ndarray:
+    """The quantized weights of a row-major K x M stream (K % 8 == 0,
+    M % 32 == 0) in strip order: strip g = columns 32g..32g+31, strips in
+    column order; inside strip g, record b (144 bytes) = [fp16 scales of rows
+    8b..8b+7 for group g (16 B) | byte 8j + i = byte j of row 8b+i's 16
+    payload bytes of group g].  A storage order with no counterpart in the
+    reference: every scale and payload byte of the row order appears once,
+    regrouped into 8 x 32 blocks with the payload column by column."""
+    G = M // GROUP
+    rec = np.asarray(blob, dtype=np.uint8).reshape(-1, SB_BYTES)
+    scales = rec[:, :SB_HEADER_BYTES].reshape(K, G, 2)  # flat group r*G + g
+    payload = rec[:, SB_HEADER_BYTES:].reshape(K, G, 16)
+    hdr = scales.reshape(K // 8, 8, G, 2).transpose(2, 0, 1, 3).reshape(G, K // 8, 16)
+    pay = payload.reshape(K // 8, 8, G, 16).transpose(2, 0, 3, 1).reshape(G, K // 8, 128)
+    return np.ascontiguousarray(np.concatenate([hdr, pay], axis=2)).reshape(-1)
+
+
+def decode_strips(strips, K: int, M: int) -> np.ndarray:
+    """W[K][M] as fp16 from strip order: the records' row-major payload
+    restored, then the 144-byte decoder (``src/dequant.py:116-147``) on each
+    8 x 32 block."""
+    G = M // GROUP
+    rec = np.asarray(strips, dtype=np.uint8).reshape(G, K // 8, SB_BYTES)
+    pay = rec[:, :, SB_HEADER_BYTES:].reshape(G, K // 8, 16, 8).transpose(0, 1, 3, 2).reshape(G, K // 8, 128)
+    rows = np.concatenate([rec[:, :, :SB_HEADER_BYTES], pay], axis=2).reshape(-1)
+    blocks = decode_superblocks(rows, G * K // 8).reshape(G, K // 8, 8, GROUP)
+    return np.ascontiguousarray(blocks.transpose(1, 2, 0, 3)).reshape(K, M)
 
 
 # --------------------------------------------------------------------------

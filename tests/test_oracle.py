@@ -342,3 +342,29 @@ def test_records_to_tiles_is_the_tile_permutation():
         dec = O.decode_superblocks(tiles, K * M // 256).reshape(t, K, 256)
         for j in range(t):
             assert np.array_equal(dec[j].view(np.uint16), wdq[:, 256 * j:256 * (j + 1)].view(np.uint16))
+
+
+def test_records_to_strips_is_the_strip_regrouping():
+    """Strip order (record (g, b) = scales of rows 8b..8b+7 of group g, then
+    byte 8j + i = byte j of row 8b+i's payload), pinned by a plain byte loop
+    over the row-order format's own offsets (group f = r * M/32 + g: scale at
+    byte 144*(f//8) + 2*(f%8), payload at 144*(f//8) + 16 + 16*(f%8)) and by
+    decoding the strips back to W."""
+    for K, M in ((8, 32), (16, 96), (40, 256), (64, 160)):
+        w = O.synthetic_weights(K, M, 0.05, 11 + K + M)
+        blob = O.quantize_pack_a(w).reshape(-1)
+        strips = O.records_to_strips(blob, K, M)
+        assert strips.shape == blob.shape and strips.dtype == np.uint8
+        G = M // 32
+        for g in range(G):
+            for b in range(K // 8):
+                dst = (g * (K // 8) + b) * 144
+                for i in range(8):
+                    f = (8 * b + i) * G + g
+                    sc = 144 * (f // 8) + 2 * (f % 8)
+                    pay = 144 * (f // 8) + 16 + 16 * (f % 8)
+                    assert np.array_equal(strips[dst + 2 * i:dst + 2 * i + 2], blob[sc:sc + 2])
+                    for j in range(16):
+                        assert strips[dst + 16 + 8 * j + i] == blob[pay + j]
+        wdq = O.decode_superblocks(blob, K * M // 256).reshape(K, M)
+        assert np.array_equal(O.decode_strips(strips, K, M).view(np.uint16), wdq.view(np.uint16))
