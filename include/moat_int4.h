@@ -197,11 +197,13 @@ int32_t moat_int4_gemm_tiles(const uint16_t* x_f16, const uint8_t* tiles, float*
  * order of src/dequant.py:116-147).  Strip g = columns 32g .. 32g+31 of W;
  * strips follow each other in column order, and inside strip g record b
  * (144 bytes) holds rows 8b .. 8b+7: bytes [0,16) the 8 fp16 scales of those
- * rows' group g, bytes [16 + 16i, 32 + 16i) row 8b+i's 16 payload bytes of
- * group g, in the record format's nibble order.  The q values and scales are
- * those of the row-order stream, bit for bit; a strip is one contiguous run
- * of K x 18 bytes, and the GEMM's workgroups each stream one contiguous
- * range of them.
+ * rows' group g (row order), then for each column pair j = 0..15 eight bytes
+ * at 16 + 8j: byte j of the payload of rows 8b+0, 8b+2, 8b+1, 8b+3, 8b+4,
+ * 8b+6, 8b+5, 8b+7 (in that order; low nibble column 32g+2j, high nibble
+ * 32g+2j+1, each stored as q + 8 as in the row order).  The q values and
+ * scales are those of the row-order stream, bit for bit; a strip is one
+ * contiguous run of K x 18 bytes, and the GEMM's workgroups each stream one
+ * contiguous range of them.
  *
  * moat_int4_records_to_strips: row order -> strip order (k % 8 == 0,
  * m % 32 == 0; both 16-byte aligned, not overlapping).
@@ -212,7 +214,8 @@ int32_t moat_int4_gemm_tiles(const uint16_t* x_f16, const uint8_t* tiles, float*
  * taken 8 per launch.  Workspace as for moat_int4_gemm (zeroed once, left
  * zero, shares the status word), sized by
  * moat_int4_gemm_strips_workspace_size; options: `splits` = workgroups
- * (0 automatic), `batch` = ring depth (0 automatic), the rest ignored.
+ * (0 automatic), `batch` = ring depth (2..4, 0 automatic), `waves` = waves
+ * per workgroup (4, 8 or 12; 0 automatic), the rest ignored.
  */
 int32_t moat_int4_records_to_strips(const uint8_t* superblocks, int32_t k, int32_t m, uint8_t* strips,
                                     hipStream_t stream);

@@ -422,7 +422,7 @@ struct StripPlan {
 };
 
 bool strip_options_ok(const moat_int4_gemm_options* o) {
-  return !o || (o->splits >= 0 && o->batch >= 0 && (o->waves == 0 || o->waves == 4 || o->waves == 8));
+  return !o || (o->splits >= 0 && o->batch >= 0 && (o->waves == 0 || o->waves == 4 || o->waves == 8 || o->waves == 12));
 }
 
 // Workgroups: one whole strip each when M/32 is 128..256 (nothing shared);
@@ -439,7 +439,9 @@ StripPlan plan_strips(int32_t n, int32_t k, int32_t m, const moat_int4_gemm_opti
   if (wgs > total) wgs = total;
   p.wgs = (int)wgs;
   const int rows = n < kStripRowsPerLaunch ? n : kStripRowsPerLaunch;
-  p.waves = moat::strips_waves(rows, o ? o->waves : 0);
+  // 12 waves (4-unit stages) for ranges of at most 256 units, 8 beyond
+  const int waves = o && o->waves ? o->waves : (total / wgs <= 256 ? 12 : 8);
+  p.waves = moat::strips_waves(rows, waves);
   p.depth = moat::strips_depth(rows, p.waves, o ? o->batch : 0);
   const int64_t base = total / wgs, rem = total % wgs;
   const bool shared = !(rem == 0 && base % units == 0);

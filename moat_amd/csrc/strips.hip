@@ -8,11 +8,12 @@
 //  * strip g is the 32 columns 32g .. 32g+31 of W (one quantization group per
 //    row), and the strips follow each other in column order;
 //  * inside strip g, record b (144 bytes) holds rows 8b .. 8b+7: bytes
-//    [0,16) are the 8 fp16 scales of those rows' group g; byte 16 + 8j + i is
-//    byte j of row 8b+i's 16 payload bytes of group g (column 32g + 2j in the
-//    low nibble, 32g + 2j + 1 in the high nibble, each stored as q + 8): the
-//    payload bytes column by column, so that the 8 rows of one column pair
-//    are 8 consecutive bytes.
+//    [0,16) are the 8 fp16 scales of those rows' group g; byte 16 + 8j +
+//    strip_row_pos(i) is byte j of row 8b+i's 16 payload bytes of group g
+//    (column 32g + 2j in the low nibble, 32g + 2j + 1 in the high nibble,
+//    each stored as q + 8): the payload bytes column pair by column pair, so
+//    that the 8 rows of one column pair are 8 consecutive bytes, rows in the
+//    order 0 2 1 3 4 6 5 7.
 // A strip is one contiguous run of K x 18 bytes, and 32 rows of it (a "unit",
 // one matrix-core K step) are 576 contiguous bytes.
 //
@@ -21,26 +22,29 @@
 //    an equal contiguous range of it (stream-K), which is one contiguous byte
 //    range of the records.  When M/32 is between 128 and 256 the plan gives
 //    every workgroup exactly one whole strip, and nothing is shared;
-//  * the 4 waves of a workgroup take every 4th unit of its range; each keeps a
-//    private LDS ring of `depth` stages of 16 units (9 KB, 9 global_load_lds
-//    copies of 64 x 16 bytes) and a two-stage ring of the X rows those units
-//    need, and keeps copying across strip boundaries: the ring never drains
-//    until the range ends;
+//  * the W waves of a workgroup (4, 8 or 12) take every W-th unit of its
+//    range; each keeps a private LDS ring of `depth` stages of 16, 8 or 4 units
+//    (576 bytes each, copied by global_load_lds_dwordx4) with the X rows
+//    those units need, issues every stage whole `depth` - 1 stages ahead, and
+//    keeps copying across strip boundaries: the ring never drains until the
+//    range ends;
 //  * per unit a lane (q, j) reads the 8 bytes of column pair j of rows
 //    8q .. 8q+7 (record q, one 8-byte read) and the record's 8 row scales,
-//    forms the two fp16 B operands of
-//    v_mfma_f32_16x16x32_f16 for columns 2j and 2j+1 (magic-exponent nibble
-//    decode, one v_pk_mul by the row-pair scales: fp16(f32(q - 8) * f32(s))
-//    exactly), and the A operand is X[row j][32u + 8q .. +7] from the stage;
+//    forms the two fp16 B operands of v_mfma_f32_16x16x32_f16 for columns 2j
+//    and 2j+1 (magic-exponent nibble decode straight from the loaded words
+//    and from the words shifted right by 8, one v_pk_mul by the row-pair
+//    scales: fp16(f32(q - 8) * f32(s)) exactly), and the A operand is
+//    X[row j][32u + 8q .. +7] from the stage;
 //  * where the range crosses a strip boundary the waves put their fp32
 //    accumulators in a small LDS area apart from the ring, meet at one
-//    barrier, and one wave adds the four in wave order and writes the part:
+//    barrier, and one wave adds the W sums in wave order and writes the part:
 //    a whole strip goes to Y; the first part of a range (a strip that began
 //    in an earlier workgroup's range) is stored encoded for that workgroup; the
 //    last part of a range (a strip whose first unit it holds) is the
 //    workgroup's own and, after its stream ends, it adds the later
 //    workgroups' parts in workgroup order (polling, bounded, as the
-//    record-stream kernel's hand-off does) and writes Y.  Results are
+//    record-stream kernel's hand-off does; the parts of up to two later
+//    workgroups are loaded during the last stage) and writes Y.  Results are
 //    deterministic.
 #include "stream_device.h"
 
@@ -50,6 +54,12 @@ constexpr int kStripCols = 32;
 constexpr int kUnitRows = 32;
 constexpr int kUnitBytes = 576;  // 32 rows x 18 bytes: 4 records
 constexpr int kStripMaxN = 8;
+
+// Position of row 8b+i's byte among the 8 bytes of one column pair of
+// record b: rows 0, 2, 1, 3, 4, 6, 5, 7 (bits 0 and 1 of i swapped), so that
+// bytes 0 and 2 of a 32-bit word, and of the word shifted right by 8, hold two
+// consecutive rows.  Its own inverse.
+__host__ __device__ constexpr int strip_row_pos(int i) { return (i & 4) | ((i & 1) << 1) | ((i >> 1) & 1); }
 
 struct StripParams {
   const uint16_t* x;   // [n][k] fp16, 16-byte aligned
@@ -63,25 +73,29 @@ struct StripParams {
   int y_vec;           // y 16-byte aligned
 };
 
-// Geometry of a workgroup of W waves (4 or 8) staging NX rows of X.  Wave w
-// takes units first + W*i of its workgroup's range; a stage holds 64 / W of
-// them (the workgroup's 64 consecutive units per stage round), copied with
-// ceil(36 * units / 64) global_load_lds_dwordx4 (1 KB each; 8 waves: the
-// fifth copy's upper lanes re-load its lower lanes' chunks into a spare half
-// kilobyte).  X: one row per copy with 4 waves (16 units x 64 B, rows 1088
-// bytes apart), two rows per copy with 8 waves (8 units x 64 B each, rows 512
-// bytes apart and the rows' unit and quarter order swizzled instead).
+// Geometry of a workgroup of W waves (4, 8 or 12) staging NX rows of X.
+// Wave w takes units first + W*i of its workgroup's range; one stage of a
+// wave holds 16, 8 or 4 of them (the workgroup's 64, 64 or 48 consecutive
+// units per stage round), 576 bytes each, copied by global_load_lds_dwordx4 (64 lanes x 16
+// bytes; the last copy of a stage has only as many lanes as chunks remain).
+// X: one copy per row of the units' 64-byte slices, rows 64 bytes apart
+// beyond their slices (a row's slices start 64 bytes further along the LDS
+// banks than the previous row's) and the 16-byte quarters of rows 4r..4r+3
+// XOR-permuted by r, so that one quarter of 16 rows falls on 16 different
+// 16-byte bank groups.
 template <int NX, int W>
 struct StripGeom {
-  static constexpr int kStageUnits = 64 / W;
-  static constexpr int kWLoads = (36 * kStageUnits + 63) / 64;  // 9 or 5
-  static constexpr int kWStage = 1024 * kWLoads;
-  static constexpr int kXRows = W == 4 ? NX : (NX < 2 ? 2 : NX);  // rows staged (8 waves: pairs)
-  static constexpr int kXRowBytes = W == 4 ? 1088 : 512;
-  static constexpr int kXLoads = W == 4 ? NX : kXRows / 2;
-  static constexpr int kXStage = kXRows * kXRowBytes;
+  static_assert(W == 4 || W == 8 || W == 12, "4, 8 or 12 waves");
+  static constexpr int kStageUnits = W == 12 ? 4 : 64 / W;            // 16, 8, 4
+  static constexpr int kWChunks = 36 * kStageUnits;                   // 16-byte chunks of a stage
+  static constexpr int kWLoads = (kWChunks + 63) / 64;                // 9, 5, 3
+  static constexpr int kWTail = kWChunks - 64 * (kWLoads - 1);        // lanes of the last copy: 64, 32, 16
+  static constexpr int kWStage = 16 * kWChunks;                       // 9216, 4608, 2304
+  static constexpr int kXLanes = 4 * kStageUnits;                     // lanes of a row's copy
+  static constexpr int kXRowBytes = 64 * kStageUnits + 64;
+  static constexpr int kXStage = NX * kXRowBytes;
   template <int kDepth>
-  static constexpr int wave_bytes() { return kDepth * kWStage + 2 * kXStage; }
+  static constexpr int wave_bytes() { return kDepth * (kWStage + kXStage); }
   static constexpr int kSlotBytes = NX * kStripCols * 4;  // one wave's part of a strip
   template <int kDepth>
   static constexpr size_t lds_bytes() {  // rings, slots, the status word's copies
@@ -112,12 +126,27 @@ __device__ __forceinline__ void load8_sc1(float4_t (&t)[8], const float* base, c
       : "memory");
 }
 
-// Output of one part of a strip by one wave (the part's sums of the four
+// A 16-byte device-coherent load the compiler schedules and waits for.
+__device__ __forceinline__ float4_t load16_coherent(const float* base, uint32_t byte_off) {
+  const unsigned long long* q = reinterpret_cast<const unsigned long long*>(reinterpret_cast<const uint8_t*>(base) + byte_off);
+  const unsigned long long a = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const unsigned long long b = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return float4_t{__builtin_bit_cast(float, (uint32_t)a), __builtin_bit_cast(float, (uint32_t)(a >> 32)),
+                  __builtin_bit_cast(float, (uint32_t)b), __builtin_bit_cast(float, (uint32_t)(b >> 32))};
+}
+
+// Contributions an owner may have loaded before its output (the slots of
+// workgroups p+1 .. p+kStripPrefetch).
+constexpr int kStripPrefetch = 2;
+
+// Output of one part of a strip by one wave (the part's sums of the W
 // waves are in `sl`, wave-major): lanes l < n * 8 each hold four columns of
-// one row.
+// one row.  `pre` holds the contributions of the first `npre` later
+// workgroups when the caller loaded them ahead (npre = 0: none).
 template <int NX, int W>
 __device__ __forceinline__ void strip_part_out(const StripParams& P, const float* sl, int p, int strip, bool whole,
-                                               bool owner, int last_unit, float poison) {
+                                               bool owner, int last_unit, float poison,
+                                               const float4_t (&pre)[kStripPrefetch], int npre) {
   const int lane = threadIdx.x & 63;
   const int r = lane >> 3, c4 = 4 * (lane & 7);
   const bool active = r < P.n;
@@ -137,33 +166,51 @@ __device__ __forceinline__ void strip_part_out(const StripParams& P, const float
     // add the parts of the later workgroups that hold units of this strip,
     // in workgroup order
     const int q_last = strip_owner(P, last_unit);
-    int polls = kMaxPolls;
     const float4_t zero = {0.f, 0.f, 0.f, 0.f};
-    for (int c0 = p + 1; c0 <= q_last; c0 += 8) {
-      uint32_t a[8];
+    bool done = false;
+    if (q_last - p <= npre) {  // all of them loaded ahead: use them if every one was written
+      bool ready = true;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) a[i] = (uint32_t)min(c0 + i, q_last) * slot_bytes + (active ? chunk : 0u);
-      float4_t t[8];
-      load8_sc1(t, P.slots, a);
-      bool ready;
-      for (;;) {
-        ready = true;
+      for (int i = 0; i < kStripPrefetch; ++i)
+        if (active && i < q_last - p) ready = ready && partial_ready(pre[i]);
+      if (ready) {
+#pragma unroll
+        for (int i = 0; i < kStripPrefetch; ++i)
+          if (active && i < q_last - p) v += dec_partial(pre[i]);
+#pragma unroll
+        for (int i = 0; i < kStripPrefetch; ++i)
+          if (active && i < q_last - p) store_sc1_at(P.slots, (uint32_t)(p + 1 + i) * slot_bytes + chunk, zero);
+        done = true;
+      }
+    }
+    if (!done) {
+      int polls = kMaxPolls;
+      for (int c0 = p + 1; c0 <= q_last; c0 += 8) {
+        uint32_t a[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) a[i] = (uint32_t)min(c0 + i, q_last) * slot_bytes + (active ? chunk : 0u);
+        float4_t t[8];
+        load8_sc1(t, P.slots, a);
+        bool ready;
+        for (;;) {
+          ready = true;
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+            if (active && c0 + i <= q_last) ready = ready && partial_ready(t[i]);
+          if (handoff_stop(ready, polls)) break;
+          --polls;
+          __builtin_amdgcn_s_sleep(1);
+          load8_sc1(t, P.slots, a);
+        }
+        if (handoff_gave_up(ready, polls))
+          __hip_atomic_fetch_or(P.status, kWsStatusHandoffTimeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 #pragma unroll
         for (int i = 0; i < 8; ++i)
-          if (active && c0 + i <= q_last) ready = ready && partial_ready(t[i]);
-        if (handoff_stop(ready, polls)) break;
-        --polls;
-        __builtin_amdgcn_s_sleep(1);
-        load8_sc1(t, P.slots, a);
+          if (active && c0 + i <= q_last) v += dec_partial(t[i]);
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          if (active && c0 + i <= q_last) store_sc1_at(P.slots, a[i], zero);
       }
-      if (handoff_gave_up(ready, polls))
-        __hip_atomic_fetch_or(P.status, kWsStatusHandoffTimeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-        if (active && c0 + i <= q_last) v += dec_partial(t[i]);
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-        if (active && c0 + i <= q_last) store_sc1_at(P.slots, a[i], zero);
     }
   }
   if (!active) return;
@@ -192,51 +239,33 @@ __global__ void __launch_bounds__(W * 64) int4_gemm_strips_kernel(StripParams P)
   const MagicWords mw = magic_words();
 
   // Weight copies: slot s = 64 i + lane of a stage carries chunk s % 36 of
-  // the stage's unit s / 36 (slots past the stage's units re-load chunk
-  // s % 36 of its first unit); the stage's units lie W units apart.  Units
+  // the stage's unit s / 36 (the stage's units lie W units apart); units
   // past the range re-load the stage's first unit.
   uint32_t woff[G::kWLoads], wfirst[G::kWLoads];
   int wunit[G::kWLoads];
 #pragma unroll
   for (int i = 0; i < G::kWLoads; ++i) {
-    const int s = 64 * i + lane;
-    wunit[i] = s < 36 * kSU ? s / 36 : 0;
+    const int s = min(64 * i + lane, G::kWChunks - 1);  // lanes past the last chunk copy nothing
+    wunit[i] = s / 36;
     wfirst[i] = (uint32_t)(16 * (s % 36));
     woff[i] = (uint32_t)(W * kUnitBytes * wunit[i]) + wfirst[i];
   }
-  // X copies (rows past N repeat row N - 1).  4 waves: copy n holds row n,
-  // lane l = unit l / 4, 16-byte quarter (l & 3) ^ ((n >> 1) & 3).  8 waves:
-  // copy c holds rows 2c (lanes 0-31) and 2c+1 (lanes 32-63), lane l = unit
-  // ((l & 31) >> 2) ^ (row & 1), quarter (l & 3) ^ ((row >> 1) & 3).  Either
-  // way the A-operand reads of 8 rows fall on 8 different 16-byte bank groups.
-  uint32_t xoff[G::kXLoads];
-  int xk;  // this lane's unit in an X copy
-  if constexpr (W == 4) {
-    xk = lane >> 2;
+  // X copies, one per row n (rows past N repeat row N - 1): lane l < 4 *
+  // kSU carries unit l / 4, quarter (l & 3) ^ ((n >> 2) & 3).
+  const int xk = lane >> 2;
+  uint32_t xoff[NX];
 #pragma unroll
-    for (int n = 0; n < G::kXLoads; ++n) {
-      const int row = min(n, P.n - 1);
-      const int quarter = (lane & 3) ^ ((n >> 1) & 3);
-      xoff[n] = (uint32_t)(2 * (row * P.k + 8 * quarter));
-    }
-  } else {
-    const int half = lane >> 5;
-    xk = ((lane & 31) >> 2) ^ half;  // rows of a copy: 2c + half, whose parity is half
-#pragma unroll
-    for (int c = 0; c < G::kXLoads; ++c) {
-      const int n = 2 * c + half;
-      const int row = min(n, P.n - 1);
-      const int quarter = (lane & 3) ^ ((n >> 1) & 3);
-      xoff[c] = (uint32_t)(2 * (row * P.k + 8 * quarter));
-    }
+  for (int n = 0; n < NX; ++n) {
+    const int row = min(n, P.n - 1);
+    const int quarter = (lane & 3) ^ ((n >> 2) & 3);
+    xoff[n] = (uint32_t)(2 * (row * P.k + 8 * quarter));
   }
-  // LDS reads of a unit: record q's scales and the 8 bytes of column pair j
-  // of its rows; X row j (rows past N read row N - 1, whose products are
-  // never stored)
+  // LDS reads of a unit k: record q's 8 row scales, the 8 bytes of column
+  // pair j of its rows, and X row j's quarter q (rows past N read row N - 1,
+  // whose products are never stored)
   const uint32_t rsc = 144 * q, rpay = 144 * q + 16 + 8 * j;
   const int xrow = min(j, P.n - 1);
-  const uint32_t rxq = (uint32_t)(G::kXRowBytes * xrow + 16 * (q ^ ((xrow >> 1) & 3)));
-  const int xpar = W == 4 ? 0 : (xrow & 1);  // 8 waves: unit k of row xrow sits at unit k ^ (xrow & 1)
+  const uint32_t rx = (uint32_t)(G::kXRowBytes * xrow + 16 * (q ^ ((xrow >> 2) & 3)));
 
   uint8_t* wring = smem + wave * G::template wave_bytes<kDepth>();
   uint8_t* xring = wring + kDepth * G::kWStage;
@@ -250,8 +279,8 @@ __global__ void __launch_bounds__(W * 64) int4_gemm_strips_kernel(StripParams P)
   const int first = lo + wave;  // this wave's units: first + W i
   const int cnt = first < hi ? (hi - first + W - 1) / W : 0;
   const int nst = (cnt + kSU - 1) / kSU;
-  // strip-relative unit of this wave's first unit of stage s (scalar, kept
-  // up to date stage by stage)
+  // strip-relative unit of the first unit of the next stage to issue
+  // (scalar, kept up to date stage by stage)
   int ub_issue = first % U;
 
   auto issue_w = [&](int s) {
@@ -259,29 +288,64 @@ __global__ void __launch_bounds__(W * 64) int4_gemm_strips_kernel(StripParams P)
     const uint8_t* base = P.w + (uint64_t)u0 * kUnitBytes;
     const uint32_t st = __builtin_amdgcn_readfirstlane(wring_lds + (s % kDepth) * G::kWStage);
 #pragma unroll
-    for (int i = 0; i < G::kWLoads; ++i)
-      lds_dma16(base, u0 + W * wunit[i] < hi ? woff[i] : wfirst[i], st + 1024 * i);
+    for (int i = 0; i < G::kWLoads; ++i) {
+      const uint32_t off = u0 + W * wunit[i] < hi ? woff[i] : wfirst[i];
+      if (i < G::kWLoads - 1 || lane < G::kWTail) lds_dma16(base, off, st + 1024 * i);
+    }
   };
   auto issue_x = [&](int s, int ub) {  // ub: strip-relative unit of the stage's first unit
     int t = ub + W * xk;
     if (t >= U) t -= U;  // U >= 64 > W * xk
-    const uint32_t st = __builtin_amdgcn_readfirstlane(xring_lds + (s & 1) * G::kXStage);
+    const uint32_t st = __builtin_amdgcn_readfirstlane(xring_lds + (s % kDepth) * G::kXStage);
 #pragma unroll
-    for (int c = 0; c < G::kXLoads; ++c)
-      lds_dma16(P.x, xoff[c] + 64u * (uint32_t)t, st + (W == 4 ? G::kXRowBytes : 2 * G::kXRowBytes) * c);
+    for (int n = 0; n < NX; ++n)
+      if (lane < G::kXLanes) lds_dma16(P.x, xoff[n] + 64u * (uint32_t)t, st + G::kXRowBytes * n);
   };
 
+  // Stages go out whole (weights, then X), kDepth - 1 ahead of the one in
+  // use: copies complete in issue order, so the wait for stage s leaves
+  // exactly the later stages in flight.
+  auto issue = [&](int s) {
+    issue_w(s);
+    issue_x(s, ub_issue);
+    ub_issue += W * kSU;
+    while (ub_issue >= U) ub_issue -= U;
+  };
 #pragma unroll
   for (int s = 0; s < kDepth - 1; ++s)
-    if (s < nst) issue_w(s);
-  if (nst > 0) issue_x(0, ub_issue);
-  else wait_vmcnt<0>();  // no ring wait will cover the status copy
+    if (s < nst) issue(s);
+  if (nst == 0) wait_vmcnt<0>();  // no ring wait will cover the status copy
 
   // parts of the range: one per strip it touches, in order
   const int strip0 = lo / U;
   const int nparts = hi > lo ? (hi - 1) / U - strip0 + 1 : 0;
   int part = 0;
   int part_end = min(hi, (strip0 + 1) * U);
+
+  // The wave that writes the range's last part, when that part begins a
+  // strip that later workgroups finish, loads their contributions during
+  // its last stage (they stored them at the start of their ranges), so that
+  // the loads' latency overlaps arithmetic instead of following it.
+  float4_t pre[kStripPrefetch] = {};
+  int npre = 0, pre_cnt = 0;
+  uint32_t pre_chunk = 0, pre_slot_bytes = 0;
+  if (nparts > 0 && wave == (nparts - 1) % W) {
+    const int strip = strip0 + nparts - 1;
+    const bool starts = max(lo, strip * U) == strip * U, ends = min(hi, (strip + 1) * U) == (strip + 1) * U;
+    if (starts && !ends) {
+      pre_cnt = strip_owner(P, (strip + 1) * U - 1) - p;
+      const int r = lane >> 3;
+      pre_chunk = r < P.n ? (uint32_t)(4 * (r * kStripCols + 4 * (lane & 7))) : 0u;
+      pre_slot_bytes = (uint32_t)(4 * P.n * kStripCols);
+    }
+  }
+  auto prefetch = [&]() {
+    if (pre_cnt < 1 || pre_cnt > kStripPrefetch) return;
+#pragma unroll
+    for (int i = 0; i < kStripPrefetch; ++i)
+      if (i < pre_cnt) pre[i] = load16_coherent(P.slots, (uint32_t)(p + 1 + i) * pre_slot_bytes + pre_chunk);
+    npre = pre_cnt;
+  };
 
   float4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
 
@@ -297,13 +361,14 @@ __global__ void __launch_bounds__(W * 64) int4_gemm_strips_kernel(StripParams P)
     acc0 = float4_t{0.f, 0.f, 0.f, 0.f};
     acc1 = float4_t{0.f, 0.f, 0.f, 0.f};
     lds_barrier();
-    if (wave == (pi & (W - 1))) {
+    if (wave == pi % W) {
       const int strip = strip0 + pi;
       const int a = max(lo, strip * U), b = min(hi, (strip + 1) * U);
       const bool whole = a == strip * U && b == (strip + 1) * U;
       const bool owner = !whole && a == strip * U;
       strip_part_out<NX, W>(P, slots + (pi & 1) * W * NX * kStripCols, p, strip, whole, owner,
-                         (strip + 1) * U - 1, status_poison(status_from_lds(lds_status)));
+                            (strip + 1) * U - 1, status_poison(status_from_lds(lds_status)), pre,
+                            pi == nparts - 1 ? npre : 0);
     }
   };
 
@@ -315,23 +380,23 @@ __global__ void __launch_bounds__(W * 64) int4_gemm_strips_kernel(StripParams P)
     uint4 sc;
     uint2 b;
   };
-  auto load_unit = [&](UnitRegs& r, const uint8_t* wu, const uint8_t* xst, int k) {
-    r.a = *reinterpret_cast<const half8_t*>(xst + 64 * (k ^ xpar) + rxq);
+  auto load_unit = [&](UnitRegs& r, const uint8_t* wu, const uint8_t* xu) {
+    r.a = *reinterpret_cast<const half8_t*>(xu + rx);
     r.sc = *reinterpret_cast<const uint4*>(wu + rsc);
     r.b = *reinterpret_cast<const uint2*>(wu + rpay);
   };
   auto math_unit = [&](const UnitRegs& r) {
+    // r.b.x holds rows 0, 2, 1, 3 of column pair j (low nibble: column 2j,
+    // high: 2j+1), r.b.y rows 4, 6, 5, 7: bytes 0 and 2 of a word and of the
+    // word shifted right by 8 are the row pairs (0,1), (2,3), (4,5), (6,7)
+    const uint32_t words[4] = {r.b.x, r.b.x >> 8, r.b.y, r.b.y >> 8};
     const uint32_t scp[4] = {r.sc.x, r.sc.y, r.sc.z, r.sc.w};  // (s_{2p}, s_{2p+1}) per row pair
     half2_t lo2[4], hi2[4];
 #pragma unroll
     for (int pp = 0; pp < 4; ++pp) {
-      // [row 2p byte, 0, row 2p+1 byte, 0]
-      const uint32_t src = pp < 2 ? r.b.x : r.b.y;
-      const uint32_t sel = (0x0Cu << 24) | ((uint32_t)(2 * (pp & 1) + 1) << 16) | (0x0Cu << 8) | (uint32_t)(2 * (pp & 1));
-      const uint32_t wpair = __builtin_amdgcn_perm(0u, src, sel);
       const half2_t s2 = bitcast<half2_t>(scp[pp]);
-      lo2[pp] = nib_lo_pair(wpair, mw.lo) * s2;
-      hi2[pp] = nib_hi_pair(wpair, mw.hi) * s2;
+      lo2[pp] = nib_lo_pair(words[pp], mw.lo) * s2;
+      hi2[pp] = nib_hi_pair(words[pp], mw.hi) * s2;
     }
     half8_t b0, b1;
 #pragma unroll
@@ -344,31 +409,29 @@ __global__ void __launch_bounds__(W * 64) int4_gemm_strips_kernel(StripParams P)
     acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(r.a, b0, acc0, 0, 0, 0);
     acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(r.a, b1, acc1, 0, 0, 0);
   };
-  auto compute = [&](const uint8_t* wu, const uint8_t* xst, int k) {
+  auto compute = [&](const uint8_t* wu, const uint8_t* xu) {
     UnitRegs r;
-    load_unit(r, wu, xst, k);
+    load_unit(r, wu, xu);
     math_unit(r);
   };
 
-  constexpr int kLW = G::kWLoads, kLX = G::kXLoads;
+  constexpr int kLS = G::kWLoads + NX;  // copies per stage
   for (int s = 0; s < nst; ++s) {
-    const bool w_more = s + kDepth - 1 < nst;
-    const bool x_more = s + 1 < nst;
-    int ub_next = ub_issue + W * kSU;
-    while (ub_next >= U) ub_next -= U;
-    if (w_more) issue_w(s + kDepth - 1);
-    if (x_more) issue_x(s + 1, ub_next);
-    ub_issue = ub_next;
-    // copies issued after this stage's X: the next X and, further ahead, weights
-    if (w_more) wait_vmcnt<kLW + kLX>();
-    else if (x_more) wait_vmcnt<kLX>();
+    if (s + kDepth - 1 < nst) issue(s + kDepth - 1);
+    // stages issued after this one
+    const int ahead = min(kDepth - 1, nst - 1 - s);
+    if (ahead >= 3) wait_vmcnt<3 * kLS>();
+    else if (ahead == 2) wait_vmcnt<2 * kLS>();
+    else if (ahead == 1) wait_vmcnt<kLS>();
     else wait_vmcnt<0>();
+    if (s == nst - 1) prefetch();  // no ring wait follows
     const uint8_t* wst = wring + (s % kDepth) * G::kWStage;
-    const uint8_t* xst = xring + (s & 1) * G::kXStage;
+    const uint8_t* xst = xring + (s % kDepth) * G::kXStage;
     const int kmax = min(kSU, cnt - kSU * s);
     // units k < kb of this stage belong to the current part; with 64 or
     // more units per strip, a stage (units at most 60 apart) meets at most
     // one part boundary
+    static_assert(W * (kSU - 1) < 64, "a stage spans fewer units than a strip");
     int kb = part_end - (first + W * kSU * s);
     kb = kb <= 0 ? 0 : min(kmax, (kb + W - 1) / W);
     // units [k_begin, k_end) of the stage: batches of 4 units, every read
@@ -381,13 +444,13 @@ __global__ void __launch_bounds__(W * 64) int4_gemm_strips_kernel(StripParams P)
         if (k0 >= k_begin && k0 + kBatch <= k_end) {
           UnitRegs r[kBatch];
 #pragma unroll
-          for (int u = 0; u < kBatch; ++u) load_unit(r[u], wst + kUnitBytes * (k0 + u), xst, k0 + u);
+          for (int u = 0; u < kBatch; ++u) load_unit(r[u], wst + kUnitBytes * (k0 + u), xst + 64 * (k0 + u));
 #pragma unroll
           for (int u = 0; u < kBatch; ++u) math_unit(r[u]);
         } else {
 #pragma unroll
           for (int u = 0; u < kBatch; ++u)
-            if (k0 + u >= k_begin && k0 + u < k_end) compute(wst + kUnitBytes * (k0 + u), xst, k0 + u);
+            if (k0 + u >= k_begin && k0 + u < k_end) compute(wst + kUnitBytes * (k0 + u), xst + 64 * (k0 + u));
         }
       }
     };
@@ -407,28 +470,55 @@ __global__ void __launch_bounds__(W * 64) int4_gemm_strips_kernel(StripParams P)
 // ---------------------------------------------------------------------------
 // Host side.
 
+constexpr size_t kStripMaxLds = 156 * 1024;
+
 template <int NX, int kDepth, int W>
 static hipError_t launch_strips_one(const StripParams& P, int wgs, hipStream_t stream) {
   const size_t lds = StripGeom<NX, W>::template lds_bytes<kDepth>();
-  if (lds > 156 * 1024) return hipErrorInvalidValue;  // never launch past the LDS
+  if (lds > kStripMaxLds) return hipErrorInvalidValue;  // never launch past the LDS
   hipLaunchKernelGGL((int4_gemm_strips_kernel<NX, kDepth, W>), dim3(wgs), dim3(W * 64), lds, stream, P);
   return hipGetLastError();
 }
 
-// X rows staged: N rounded up to 1, 2, 4 or 8.  Waves: 8 (two per SIMD, so
-// that one wave's LDS and matrix-core latencies hide behind the other's
-// arithmetic) up to 4 rows, 4 beyond (the LDS holds no more).  Ring depth:
-// as deep as the LDS allows, 3 or 2.
+// X rows staged: N rounded up to 1, 2, 4 or 8.  Waves: 4, 8 or 12 (8 rows:
+// 4 or 12, the LDS holds no 8-wave ring of them).  A single wave issues a
+// vector instruction at most every other cycle slot, so that two or three
+// waves a SIMD hide each other's LDS and matrix-core latencies; the plan
+// picks 12 for short ranges (their 4-unit stages ramp up sooner), 8 for
+// longer ones, and 4 for 8 rows (12 waves copy 8 rows as 8 narrow copies a
+// stage, measured slower).  Ring depth 2 unless the caller asks for more (one
+// stage in flight a wave keeps the HBM busy; deeper rings measured slower).
 int strips_rows_staged(int n) { return n <= 1 ? 1 : n <= 2 ? 2 : n <= 4 ? 4 : 8; }
 int strips_waves(int n, int waves) {
-  if (strips_rows_staged(n) == 8) return 4;
-  return waves == 4 || waves == 8 ? waves : 8;
+  if (strips_rows_staged(n) == 8) return waves == 12 ? 12 : 4;
+  return waves == 4 || waves == 12 ? waves : 8;
+}
+template <int NX, int W>
+static int strips_max_depth() {
+  static_assert(StripGeom<NX, W>::template lds_bytes<2>() <= kStripMaxLds, "a two-stage ring must fit");
+  return StripGeom<NX, W>::template lds_bytes<4>() <= kStripMaxLds   ? 4
+         : StripGeom<NX, W>::template lds_bytes<3>() <= kStripMaxLds ? 3
+                                                                      : 2;
 }
 int strips_depth(int n, int waves, int depth) {
   const int nx = strips_rows_staged(n);
   const int w = strips_waves(n, waves);
-  const int max_depth = w == 8 ? (nx <= 2 ? 3 : 2) : (nx <= 4 ? 3 : 2);
-  return depth <= 0 || depth > max_depth ? max_depth : (depth < 2 ? 2 : depth);
+  int max_depth = 2;
+  if (w == 12) max_depth = nx == 1 ? strips_max_depth<1, 12>() : nx == 2 ? strips_max_depth<2, 12>()
+                          : nx == 4 ? strips_max_depth<4, 12>() : strips_max_depth<8, 12>();
+  else if (w == 8) max_depth = nx == 1 ? strips_max_depth<1, 8>() : nx == 2 ? strips_max_depth<2, 8>() : strips_max_depth<4, 8>();
+  else max_depth = nx == 1 ? strips_max_depth<1, 4>() : nx == 2 ? strips_max_depth<2, 4>()
+                   : nx == 4 ? strips_max_depth<4, 4>() : strips_max_depth<8, 4>();
+  return depth <= 2 ? 2 : depth > max_depth ? max_depth : depth;
+}
+
+template <int NX, int W>
+static hipError_t launch_strips_w(const StripParams& P, int wgs, int depth, hipStream_t stream) {
+  if constexpr (StripGeom<NX, W>::template lds_bytes<4>() <= kStripMaxLds)
+    if (depth >= 4) return launch_strips_one<NX, 4, W>(P, wgs, stream);
+  if constexpr (StripGeom<NX, W>::template lds_bytes<3>() <= kStripMaxLds)
+    if (depth >= 3) return launch_strips_one<NX, 3, W>(P, wgs, stream);
+  return launch_strips_one<NX, 2, W>(P, wgs, stream);
 }
 
 hipError_t launch_gemm_strips(const uint16_t* x, const uint8_t* w, float* y, int n, int k, int m, int wgs, int depth,
@@ -444,15 +534,21 @@ hipError_t launch_gemm_strips(const uint16_t* x, const uint8_t* w, float* y, int
   const int nx = strips_rows_staged(n);
   waves = strips_waves(n, waves);
   depth = strips_depth(n, waves, depth);
-  if (waves == 8) {
-    if (nx == 1) return depth >= 3 ? launch_strips_one<1, 3, 8>(P, wgs, stream) : launch_strips_one<1, 2, 8>(P, wgs, stream);
-    if (nx == 2) return depth >= 3 ? launch_strips_one<2, 3, 8>(P, wgs, stream) : launch_strips_one<2, 2, 8>(P, wgs, stream);
-    return launch_strips_one<4, 2, 8>(P, wgs, stream);
+  if (waves == 12) {
+    if (nx == 1) return launch_strips_w<1, 12>(P, wgs, depth, stream);
+    if (nx == 2) return launch_strips_w<2, 12>(P, wgs, depth, stream);
+    if (nx == 4) return launch_strips_w<4, 12>(P, wgs, depth, stream);
+    return launch_strips_w<8, 12>(P, wgs, depth, stream);
   }
-  if (nx == 1) return depth >= 3 ? launch_strips_one<1, 3, 4>(P, wgs, stream) : launch_strips_one<1, 2, 4>(P, wgs, stream);
-  if (nx == 2) return depth >= 3 ? launch_strips_one<2, 3, 4>(P, wgs, stream) : launch_strips_one<2, 2, 4>(P, wgs, stream);
-  if (nx == 4) return depth >= 3 ? launch_strips_one<4, 3, 4>(P, wgs, stream) : launch_strips_one<4, 2, 4>(P, wgs, stream);
-  return launch_strips_one<8, 2, 4>(P, wgs, stream);
+  if (waves == 8) {
+    if (nx == 1) return launch_strips_w<1, 8>(P, wgs, depth, stream);
+    if (nx == 2) return launch_strips_w<2, 8>(P, wgs, depth, stream);
+    return launch_strips_w<4, 8>(P, wgs, depth, stream);
+  }
+  if (nx == 1) return launch_strips_w<1, 4>(P, wgs, depth, stream);
+  if (nx == 2) return launch_strips_w<2, 4>(P, wgs, depth, stream);
+  if (nx == 4) return launch_strips_w<4, 4>(P, wgs, depth, stream);
+  return launch_strips_w<8, 4>(P, wgs, depth, stream);
 }
 
 // Records of W[K][M] from row order to strip order: one thread per 16-byte
@@ -478,15 +574,17 @@ __global__ void records_to_strips_kernel(const uint8_t* __restrict__ src, int64_
       }
       dst[e] = uint4{h[0], h[1], h[2], h[3]};
     } else {
-      // output byte e < 8: byte j0 of row 8b+e; e >= 8: byte j0+1 of row 8b+e-8
+      // output bytes 0-7: byte j0 of rows 8b .. 8b+7, bytes 8-15: byte j0+1,
+      // row i at position strip_row_pos(i)
       const int64_t j0 = 2 * (c - 1);
       uint32_t lo[2] = {0u, 0u}, hi[2] = {0u, 0u};
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const int64_t f = (8 * b + i) * gpr + g;
         const uint32_t two = *reinterpret_cast<const uint16_t*>(src + group_payload_offset(f) + j0);
-        lo[i >> 2] |= (two & 0xFFu) << (8 * (i & 3));
-        hi[i >> 2] |= (two >> 8) << (8 * (i & 3));
+        const int pos = strip_row_pos(i);
+        lo[pos >> 2] |= (two & 0xFFu) << (8 * (pos & 3));
+        hi[pos >> 2] |= (two >> 8) << (8 * (pos & 3));
       }
       dst[e] = uint4{lo[0], lo[1], hi[0], hi[1]};
     }

@@ -270,20 +270,29 @@ def records_to_tiles(blob, K: int, M: int) -> np.ndarray:
     return np.ascontiguousarray(rec.transpose(1, 0, 2)).reshape(-1)
 
 
+# Position of row 8b+i's byte inside the 8 bytes of one column pair of a
+# strip-order record (rows 0-3 in the order 0, 2, 1, 3, rows 4-7 likewise):
+# bytes 0 and 2 of each little-endian 32-bit word then hold two consecutive
+# rows, and bytes 1 and 3 the next two.  The map is its own inverse.
+STRIP_ROW_POS = np.array([0, 2, 1, 3, 4, 6, 5, 7])
+
+
 def records_to_strips(blob, K: int, M: int) -> np.ndarray:
     """The quantized weights of a row-major K x M stream (K % 8 == 0,
     M % 32 == 0) in strip order: strip g = columns 32g..32g+31, strips in
     column order; inside strip g, record b (144 bytes) = [fp16 scales of rows
-    8b..8b+7 for group g (16 B) | byte 8j + i = byte j of row 8b+i's 16
-    payload bytes of group g].  A storage order with no counterpart in the
-    reference: every scale and payload byte of the row order appears once,
-    regrouped into 8 x 32 blocks with the payload column by column."""
+    8b..8b+7 for group g (16 B) | byte 8j + STRIP_ROW_POS[i] = byte j of row
+    8b+i's 16 payload bytes of group g].  A storage order with no counterpart
+    in the reference: every scale and payload byte of the row order appears
+    once, regrouped into 8 x 32 blocks with the payload column pair by column
+    pair."""
     G = M // GROUP
     rec = np.asarray(blob, dtype=np.uint8).reshape(-1, SB_BYTES)
     scales = rec[:, :SB_HEADER_BYTES].reshape(K, G, 2)  # flat group r*G + g
     payload = rec[:, SB_HEADER_BYTES:].reshape(K, G, 16)
     hdr = scales.reshape(K // 8, 8, G, 2).transpose(2, 0, 1, 3).reshape(G, K // 8, 16)
-    pay = payload.reshape(K // 8, 8, G, 16).transpose(2, 0, 3, 1).reshape(G, K // 8, 128)
+    pay = payload.reshape(K // 8, 8, G, 16).transpose(2, 0, 3, 1)  # [g, b, byte j, row i]
+    pay = pay[:, :, :, STRIP_ROW_POS].reshape(G, K // 8, 128)      # position p holds row STRIP_ROW_POS[p]
     return np.ascontiguousarray(np.concatenate([hdr, pay], axis=2)).reshape(-1)
 
 
@@ -293,7 +302,8 @@ def decode_strips(strips, K: int, M: int) -> np.ndarray:
     8 x 32 block."""
     G = M // GROUP
     rec = np.asarray(strips, dtype=np.uint8).reshape(G, K // 8, SB_BYTES)
-    pay = rec[:, :, SB_HEADER_BYTES:].reshape(G, K // 8, 16, 8).transpose(0, 1, 3, 2).reshape(G, K // 8, 128)
+    pay = rec[:, :, SB_HEADER_BYTES:].reshape(G, K // 8, 16, 8)[:, :, :, STRIP_ROW_POS]  # [g, b, byte j, row i]
+    pay = pay.transpose(0, 1, 3, 2).reshape(G, K // 8, 128)
     rows = np.concatenate([rec[:, :, :SB_HEADER_BYTES], pay], axis=2).reshape(-1)
     blocks = decode_superblocks(rows, G * K // 8).reshape(G, K // 8, 8, GROUP)
     return np.ascontiguousarray(blocks.transpose(1, 2, 0, 3)).reshape(K, M)

@@ -85,7 +85,7 @@ def test_strip_gemm_matches_oracle(K, M, ns):
 @pytest.mark.parametrize("K,M", [(2048, 2048), (3072, 8192), (2048, 1024)])
 def test_strip_gemm_forced_plans(K, M):
     """Workgroup counts that make ranges start and end anywhere in a strip,
-    both ring depths and both wave counts (N=8 always runs on 4 waves)."""
+    ring depths 2 and 3 and every wave count (N=8 always runs on 4 waves)."""
     from moat_amd.dequant import batched_int4_matmul, records_to_strips
     blob, wdq = problem(K, M, 9 + K + M)
     strips = records_to_strips(torch.from_numpy(blob).cuda(), K, M)
@@ -95,7 +95,7 @@ def test_strip_gemm_forced_plans(K, M):
         xd = torch.from_numpy(x).cuda()
         for splits in (1, 2, 3, 7, 33, 100, 255, 256):
             for depth in (2, 3):
-                for waves in (4, 8):
+                for waves in (4, 8, 12):
                     say(f"case: strip gemm K={K} M={M} N={N} workgroups={splits} depth={depth} waves={waves}")
                     y = batched_int4_matmul(xd, strips, K, M, strip_order=True, splits=splits, batch=depth,
                                             waves=waves)

@@ -346,7 +346,8 @@ def test_records_to_tiles_is_the_tile_permutation():
 
 def test_records_to_strips_is_the_strip_regrouping():
     """Strip order (record (g, b) = scales of rows 8b..8b+7 of group g, then
-    byte 8j + i = byte j of row 8b+i's payload), pinned by a plain byte loop
+    byte 8j + pos(i) = byte j of row 8b+i's payload, pos = 0 2 1 3 4 6 5 7),
+    pinned by a plain byte loop
     over the row-order format's own offsets (group f = r * M/32 + g: scale at
     byte 144*(f//8) + 2*(f%8), payload at 144*(f//8) + 16 + 16*(f%8)) and by
     decoding the strips back to W."""
@@ -364,7 +365,8 @@ def test_records_to_strips_is_the_strip_regrouping():
                     sc = 144 * (f // 8) + 2 * (f % 8)
                     pay = 144 * (f // 8) + 16 + 16 * (f % 8)
                     assert np.array_equal(strips[dst + 2 * i:dst + 2 * i + 2], blob[sc:sc + 2])
+                    pos = (0, 2, 1, 3, 4, 6, 5, 7)[i]
                     for j in range(16):
-                        assert strips[dst + 16 + 8 * j + i] == blob[pay + j]
+                        assert strips[dst + 16 + 8 * j + pos] == blob[pay + j]
         wdq = O.decode_superblocks(blob, K * M // 256).reshape(K, M)
         assert np.array_equal(O.decode_strips(strips, K, M).view(np.uint16), wdq.view(np.uint16))
