@@ -54,6 +54,9 @@ hipError_t launch_gemm_strips(const uint16_t* x, const uint8_t* w, float* y, int
 hipError_t launch_records_to_strips(const uint8_t* sb, int k, int m, uint8_t* strips, hipStream_t stream);
 int strips_waves(int n, int waves);
 int strips_depth(int n, int waves, int depth);
+hipError_t launch_gemm_strip_groups(const uint16_t* x, const uint8_t* w, float* y, int n, int k, int m, int wgs,
+                                    int depth, float* slots, uint32_t* status, hipStream_t stream);
+int strip_groups_slot_bytes(int n);
 }  // namespace moat
 
 namespace {
@@ -415,6 +418,7 @@ bool strips_shape_ok(int32_t n, int32_t k, int32_t m) {
 }
 
 struct StripPlan {
+  bool groups;  // N > 8 in one launch of the strip-group kernel
   int wgs;
   int depth;
   int waves;
@@ -425,13 +429,37 @@ bool strip_options_ok(const moat_int4_gemm_options* o) {
   return !o || (o->splits >= 0 && o->batch >= 0 && (o->waves == 0 || o->waves == 4 || o->waves == 8 || o->waves == 12));
 }
 
-// Workgroups: one whole strip each when M/32 is 128..256 (nothing shared);
-// otherwise up to 256 (one per CU: the kernel's LDS leaves room for one),
-// at least 16 units each.  Shared strips need the status word and one slot
-// of 8 x 32 floats per workgroup, after the fixed 64 KB block.
+// N <= 8: the strip kernel.  Workgroups: one whole strip each when M/32 is
+// 128..256 (nothing shared); otherwise up to 256 (one per CU: the kernel's
+// LDS leaves room for one), at least 16 units each.  Shared strips need the
+// status word and one slot of 8 x 32 floats per workgroup, after the fixed
+// 64 KB block.
+// N > 8: the strip-group kernel over (group of 8 strips, unit) items when the
+// records span fewer than 2^32 bytes (its copy offsets are 32-bit; larger
+// matrices run the strip kernel 8 rows at a time): up to 256 workgroups of
+// at least 16 items, and slots of 8 waves x 2 or 4 KB per workgroup.
 StripPlan plan_strips(int32_t n, int32_t k, int32_t m, const moat_int4_gemm_options* o) {
   StripPlan p;
-  const int64_t strips = m / 32, units = k / 32, total = strips * units;
+  const int64_t strips = m / 32, units = k / 32;
+  // (two 8-row launches of the strip kernel measured faster than one
+  // strip-group launch for 9..16 rows of matrices under 2^26 weights)
+  const bool small16 = n <= 16 && (int64_t)k * m < ((int64_t)1 << 26);
+  p.groups = n > kStripRowsPerLaunch && !small16 && strips * units * 576 < ((int64_t)1 << 32);
+  if (p.groups) {
+    const int64_t total = (strips + 7) / 8 * units;
+    int64_t wgs;
+    if (o && o->splits > 0) wgs = o->splits < kStripMaxWorkgroups ? o->splits : kStripMaxWorkgroups;
+    else wgs = total / 16 < 256 ? (total / 16 > 0 ? total / 16 : 1) : 256;
+    if (wgs > total) wgs = total;
+    p.wgs = (int)wgs;
+    p.depth = o && o->batch == 2 ? 2 : 3;  // 3 measured faster on long ranges, equal on short ones
+    p.waves = 8;
+    const int64_t base = total / wgs, rem = total % wgs;
+    const bool shared = !(rem == 0 && base % units == 0);
+    p.workspace_bytes = shared ? kCounterBlockBytes + wgs * 8 * (int64_t)moat::strip_groups_slot_bytes(n) : 0;
+    return p;
+  }
+  const int64_t total = strips * units;
   int64_t wgs;
   if (o && o->splits > 0) wgs = o->splits < kStripMaxWorkgroups ? o->splits : kStripMaxWorkgroups;
   else if (strips >= 128 && strips <= 256) wgs = strips;
@@ -531,6 +559,9 @@ int32_t moat_int4_gemm_strips(const uint16_t* x_f16, const uint8_t* strips, floa
     status = static_cast<uint32_t*>(workspace);
     slots = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + kCounterBlockBytes);
   }
+  if (p.groups)
+    return status_of(moat::launch_gemm_strip_groups(x_f16, strips, y_f32, n, k, m, p.wgs, p.depth, slots, status,
+                                                    stream));
   // 8 rows of X per launch; the launches share the workspace in stream order
   for (int32_t r0 = 0; r0 < n; r0 += kStripRowsPerLaunch) {
     const int32_t rows = n - r0 < kStripRowsPerLaunch ? n - r0 : kStripRowsPerLaunch;

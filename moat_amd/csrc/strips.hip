@@ -126,7 +126,24 @@ __device__ __forceinline__ void load8_sc1(float4_t (&t)[8], const float* base, c
       : "memory");
 }
 
-// A 16-byte device-coherent load the compiler schedules and waits for.
+// 16-byte device-coherent accesses (two agent-scope 8-byte atomics, sc1)
+// that the compiler schedules and waits for itself.
+__device__ __forceinline__ float4_t load16_coherent(const float4_t* p) {
+  const unsigned long long* q = reinterpret_cast<const unsigned long long*>(p);
+  const unsigned long long a = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const unsigned long long b = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return float4_t{__builtin_bit_cast(float, (uint32_t)a), __builtin_bit_cast(float, (uint32_t)(a >> 32)),
+                  __builtin_bit_cast(float, (uint32_t)b), __builtin_bit_cast(float, (uint32_t)(b >> 32))};
+}
+// (The elements go through __float_as_uint: this compiler evaluates
+// __builtin_bit_cast applied directly to a vector element as element 0.)
+__device__ __forceinline__ void store16_coherent(float4_t* p, float4_t v) {
+  unsigned long long* q = reinterpret_cast<unsigned long long*>(p);
+  const unsigned long long a = (unsigned long long)__float_as_uint(v[0]) | ((unsigned long long)__float_as_uint(v[1]) << 32);
+  const unsigned long long b = (unsigned long long)__float_as_uint(v[2]) | ((unsigned long long)__float_as_uint(v[3]) << 32);
+  __hip_atomic_store(q, a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(q + 1, b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 __device__ __forceinline__ float4_t load16_coherent(const float* base, uint32_t byte_off) {
   const unsigned long long* q = reinterpret_cast<const unsigned long long*>(reinterpret_cast<const uint8_t*>(base) + byte_off);
   const unsigned long long a = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -549,6 +566,354 @@ hipError_t launch_gemm_strips(const uint16_t* x, const uint8_t* w, float* y, int
   if (nx == 2) return launch_strips_w<2, 4>(P, wgs, depth, stream);
   if (nx == 4) return launch_strips_w<4, 4>(P, wgs, depth, stream);
   return launch_strips_w<8, 4>(P, wgs, depth, stream);
+}
+
+// ---------------------------------------------------------------------------
+// Strip groups: the GEMM over strip order for 9 <= N <= 32 in one pass.
+//  * strips are taken 8 at a time (a group, 256 columns); the (group, unit)
+//    items form one stream (group-major), and workgroup p takes an equal
+//    contiguous range of it, as the strip kernel does with units;
+//  * the 8 waves of a workgroup walk the range's units together, wave w on
+//    strip 8g + w of the unit's group g: each keeps a private ring of
+//    `depth` stages of 4 units (2304 bytes), and the X rows of a stage's 4
+//    units (N rounded up to 16 or 32, 256 bytes a row) are staged once for
+//    all 8 waves (one 1 KB copy per wave), behind one barrier a stage;
+//  * per unit a wave decodes its strip's 32 x 32 block exactly as the strip
+//    kernel does and multiplies it by one or two 16-row tiles of X
+//    (v_mfma_f32_16x16x32_f16, the decoded operands reused by both tiles);
+//  * a wave owns its strip's sums: at a group boundary it writes them to Y
+//    (whole), or stores them (device-coherent) for the workgroup that began
+//    the group -- the workgroup's waves meet at a barrier and wave 0 raises
+//    the workgroup's flag with an agent-scope release -- or, owning the
+//    group's start, waits for every later workgroup's flag (wave 0, bounded
+//    polling as in the strip kernel's hand-off), acquires once (the L2 may
+//    hold stale copies of their slots), shares the outcome through LDS, and
+//    every wave loads and adds their sums in workgroup order, zeroes their
+//    slots and writes Y.  No cross-wave sums.  (The sums travel as
+//    plain fp32 behind a flag rather than complement-encoded like the strip
+//    kernel's: encoding the accumulators in place gave wrong words in a few
+//    lanes on the GPU, a schedule-dependent failure traced to the encode and
+//    not further; the flag protocol has no such step.)
+constexpr int kGroupWaves = 8;       // strips of a group, one a wave
+constexpr int kGroupStageUnits = 4;  // units of a stage
+constexpr int kGroupWStage = kGroupStageUnits * kUnitBytes;       // 2304: 2 full copies + 16 lanes
+constexpr int kGroupWLoads = (36 * kGroupStageUnits + 63) / 64;   // 3
+constexpr int kGroupWTail = 36 * kGroupStageUnits - 64 * (kGroupWLoads - 1);  // 16
+
+struct GroupParams {
+  const uint16_t* x;   // [n][k] fp16, 16-byte aligned
+  const uint8_t* w;    // strip-order records (fewer than 2^32 bytes)
+  float* y;            // [n][m] fp32
+  float* slots;        // per (workgroup, wave) NT x 2 KB of fp32 sums; null when nothing is shared
+  uint32_t* status;    // workspace status word, followed after 256 bytes by one flag word per
+                       // workgroup; null when nothing is shared
+  int n, k, m;
+  int units;           // units per strip, k / 32
+  int strips;          // m / 32
+  int base, rem;       // workgroup p covers items [p*base + min(p, rem), +base + (p < rem))
+  int y_vec8;          // y 8-byte aligned
+};
+
+template <int NT>
+struct GroupGeom {
+  static constexpr int kRows = 16 * NT;      // X rows staged (rows past N repeat row N - 1)
+  static constexpr int kXLoads = kRows / 4;  // 1 KB copies: 4 rows x 4 units x 64 bytes
+  static constexpr int kXStage = kRows * 256;
+  static constexpr int kSlotBytes = NT * 2 * 64 * 16;  // one wave's sums: (tile, column half, lane) x 16 bytes
+  template <int kDepth>
+  static constexpr size_t lds_bytes() {
+    return kStatusLdsBytes + (size_t)kDepth * (kXStage + kGroupWaves * kGroupWStage);
+  }
+};
+
+// Workgroup holding item t of the group stream.
+__device__ __forceinline__ int group_owner(const GroupParams& P, int t) {
+  const int big = P.rem * (P.base + 1);
+  return t < big ? t / (P.base + 1) : P.rem + (t - big) / P.base;
+}
+
+template <int NT, int kDepth>
+__global__ void __launch_bounds__(kGroupWaves * 64) int4_gemm_strip_groups_kernel(GroupParams P) {
+  using G = GroupGeom<NT>;
+  constexpr int kSU = kGroupStageUnits;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int q = lane >> 4, j = lane & 15;
+  const int p = blockIdx.x;
+  const int U = P.units;
+  const int lo = p * P.base + min(p, P.rem);
+  const int hi = lo + P.base + (p < P.rem ? 1 : 0);
+  const MagicWords mw = magic_words();
+
+  uint32_t* lds_status = reinterpret_cast<uint32_t*>(smem);
+  uint8_t* xring = smem + kStatusLdsBytes;
+  uint8_t* wring = xring + kDepth * G::kXStage + wave * kDepth * kGroupWStage;
+  const uint32_t xring_lds = (uint32_t)(uintptr_t)(lds_ptr_t)xring;
+  const uint32_t wring_lds = (uint32_t)(uintptr_t)(lds_ptr_t)wring;
+  status_to_lds(P.status, lds_status);  // the oldest copy: the first ring wait covers it
+
+  // Weight copies: slot c = 64 i + lane carries chunk c % 36 of the stage's
+  // unit c / 36 (lanes past the 144 chunks copy nothing).
+  int wunit[kGroupWLoads];
+  uint32_t wchunk[kGroupWLoads];
+#pragma unroll
+  for (int i = 0; i < kGroupWLoads; ++i) {
+    const int c = min(64 * i + lane, 36 * kSU - 1);
+    wunit[i] = c / 36;
+    wchunk[i] = (uint32_t)(16 * (c % 36));
+  }
+  // X copy of this wave: rows 4xc .. 4xc+3 (waves past the copies repeat
+  // them: the same bytes to the same place).  Lane l: row 4xc + l / 16,
+  // physical unit ((l >> 2) & 3) holds unit (physical - row) & 3 of the
+  // stage, physical quarter (l & 3) holds quarter (l & 3) ^ ((row >> 2) & 3):
+  // a quarter of 16 rows falls on 16 different 16-byte bank groups.
+  const int xc = wave % G::kXLoads;
+  const int xr = 4 * xc + (lane >> 4);
+  const int xk = (((lane >> 2) & 3) - xr) & 3;
+  const uint32_t xrow_off = (uint32_t)(2 * (min(xr, P.n - 1) * P.k + 8 * ((lane & 3) ^ ((xr >> 2) & 3))));
+  // LDS reads: record q's scales and column pair j's 8 bytes of a unit; X
+  // row 16 tt + j (rows past N read row N - 1), quarter q, of unit k
+  const uint32_t rsc = 144 * q, rpay = 144 * q + 16 + 8 * j;
+  uint32_t rx[NT][kSU];
+#pragma unroll
+  for (int tt = 0; tt < NT; ++tt) {
+    const int rr = min(16 * tt + j, P.n - 1);
+#pragma unroll
+    for (int k = 0; k < kSU; ++k) rx[tt][k] = (uint32_t)(256 * rr + 64 * ((k + rr) & 3) + 16 * (q ^ ((rr >> 2) & 3)));
+  }
+
+  const int nst = (hi - lo + kSU - 1) / kSU;  // the same for every wave
+  // group and strip-relative unit of the next stage to issue (scalars)
+  int g_issue = lo / U, u_issue = lo - g_issue * U;
+  auto issue = [&](int s) {
+    const int t0 = lo + kSU * s;
+    const uint32_t wst = __builtin_amdgcn_readfirstlane(wring_lds + (s % kDepth) * kGroupWStage);
+#pragma unroll
+    for (int i = 0; i < kGroupWLoads; ++i) {
+      int g = g_issue, u = u_issue + wunit[i];
+      if (u >= U) { u -= U; ++g; }
+      if (t0 + wunit[i] >= hi) { g = g_issue; u = u_issue; }  // past the range: the stage's first unit
+      const int strip = min(kGroupWaves * g + wave, P.strips - 1);  // waves past the last strip copy a real one
+      const uint32_t off = (uint32_t)(strip * U + u) * (uint32_t)kUnitBytes + wchunk[i];
+      if (i < kGroupWLoads - 1 || lane < kGroupWTail) lds_dma16(P.w, off, wst + 1024 * i);
+    }
+    int ux = u_issue + xk;
+    if (ux >= U) ux -= U;
+    if (t0 + xk >= hi) ux = u_issue;
+    lds_dma16(P.x, xrow_off + 64u * (uint32_t)ux,
+              __builtin_amdgcn_readfirstlane(xring_lds + (s % kDepth) * G::kXStage + 1024 * xc));
+    u_issue += kSU;
+    if (u_issue >= U) { u_issue -= U; ++g_issue; }
+  };
+#pragma unroll
+  for (int s = 0; s < kDepth - 1; ++s)
+    if (s < nst) issue(s);
+  if (nst == 0) wait_vmcnt<0>();
+
+  // parts: one per group the range touches
+  int gcur = lo / U;
+  int part_end = min(hi, (gcur + 1) * U);
+  float4_t acc[NT][2];
+#pragma unroll
+  for (int tt = 0; tt < NT; ++tt) acc[tt][0] = acc[tt][1] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+  // Group boundary.  Every wave of the workgroup flushes the same part at
+  // the same point (they walk the same units), so the hand-off can use
+  // workgroup barriers: one flag and one release per contributing workgroup.
+  uint32_t* lds_flag = lds_status + 1;  // owner: the poll's outcome, for all waves
+  auto flush = [&]() {
+    const int strip = kGroupWaves * gcur + wave;
+    const int a = max(lo, gcur * U), b = min(hi, (gcur + 1) * U);
+    const bool whole = a == gcur * U && b == (gcur + 1) * U;
+    const bool owner = !whole && a == gcur * U;
+    float4_t* slots4 = reinterpret_cast<float4_t*>(P.slots);
+    uint32_t* flags = P.status + kWsStatusBytes / 4;  // one word per workgroup, zero between calls
+    constexpr int kChunks = NT * 2 * 64;               // float4 chunks of one wave's sums
+    if (!whole && !owner) {  // the first part of the range: stored for the group's first workgroup
+      if (strip < P.strips) {
+        float4_t* mine = slots4 + (size_t)(p * kGroupWaves + wave) * kChunks;
+#pragma unroll
+        for (int tt = 0; tt < NT; ++tt)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) store16_coherent(mine + (2 * tt + h) * 64 + lane, acc[tt][h]);
+      }
+      wait_vmcnt<0>();  // this wave's stores have left it
+      lds_barrier();
+      if (wave == 0)  // release: every wave's sums reach the device before the flag
+        __hip_atomic_store(flags + p, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+      bool gave_up = false;
+      if (owner) {  // add the later workgroups' sums of this group, in workgroup order
+        const int q_last = group_owner(P, (gcur + 1) * U - 1);
+        if (wave == 0) {  // every later workgroup's flag, then one acquire for all their sums
+          int polls = kMaxPolls;
+          bool all = true;
+          for (int c = p + 1; c <= q_last; ++c) {
+            bool seen;
+            for (;;) {
+              seen = __hip_atomic_load(flags + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
+              if (handoff_stop(seen, polls)) break;
+              --polls;
+              __builtin_amdgcn_s_sleep(1);
+            }
+            all = all && seen;
+            __hip_atomic_store(flags + c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
+          if (!all)
+            __hip_atomic_fetch_or(P.status, kWsStatusHandoffTimeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");  // drop cached copies of their slots
+          if (lane == 0) *lds_flag = all ? 1u : 0u;
+        }
+        lds_barrier();
+        gave_up = *reinterpret_cast<volatile uint32_t*>(lds_flag) == 0u;
+        if (strip < P.strips) {
+          for (int c = p + 1; c <= q_last; ++c) {
+            float4_t* theirs = slots4 + (size_t)(c * kGroupWaves + wave) * kChunks;
+#pragma unroll
+            for (int tt = 0; tt < NT; ++tt)
+#pragma unroll
+              for (int h = 0; h < 2; ++h) acc[tt][h] += load16_coherent(theirs + (2 * tt + h) * 64 + lane);
+            // leave the workspace as found (zero): the other kernels sharing it
+            // take any non-zero slot word for a written partial
+#pragma unroll
+            for (int tt = 0; tt < NT; ++tt)
+#pragma unroll
+              for (int h = 0; h < 2; ++h)
+                store16_coherent(theirs + (2 * tt + h) * 64 + lane, float4_t{0.f, 0.f, 0.f, 0.f});
+          }
+        }
+      }
+      if (strip < P.strips) {
+        const float poison = status_poison(status_from_lds(lds_status) | (gave_up ? 1u : 0u));
+#pragma unroll
+        for (int tt = 0; tt < NT; ++tt)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int r = 16 * tt + 4 * q + v;
+            if (r < P.n) {
+              float* yp = P.y + (int64_t)r * P.m + kStripCols * strip + 2 * j;
+              const float y0 = acc[tt][0][v] + poison, y1 = acc[tt][1][v] + poison;
+              if (P.y_vec8) {
+                *reinterpret_cast<float2*>(yp) = float2{y0, y1};
+              } else {
+                yp[0] = y0;
+                yp[1] = y1;
+              }
+            }
+          }
+      }
+    }
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt) acc[tt][0] = acc[tt][1] = float4_t{0.f, 0.f, 0.f, 0.f};
+  };
+
+  struct UnitRegs {
+    half8_t a[NT];
+    uint4 sc;
+    uint2 b;
+  };
+  auto load_unit = [&](UnitRegs& r, const uint8_t* wst, const uint8_t* xst, int k) {
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt) r.a[tt] = *reinterpret_cast<const half8_t*>(xst + rx[tt][k]);
+    r.sc = *reinterpret_cast<const uint4*>(wst + kUnitBytes * k + rsc);
+    r.b = *reinterpret_cast<const uint2*>(wst + kUnitBytes * k + rpay);
+  };
+  auto math_unit = [&](const UnitRegs& r) {
+    const uint32_t words[4] = {r.b.x, r.b.x >> 8, r.b.y, r.b.y >> 8};  // rows (0,1), (2,3), (4,5), (6,7)
+    const uint32_t scp[4] = {r.sc.x, r.sc.y, r.sc.z, r.sc.w};
+    half8_t b0, b1;
+#pragma unroll
+    for (int pp = 0; pp < 4; ++pp) {
+      const half2_t s2 = bitcast<half2_t>(scp[pp]);
+      const half2_t lo2 = nib_lo_pair(words[pp], mw.lo) * s2;
+      const half2_t hi2 = nib_hi_pair(words[pp], mw.hi) * s2;
+      b0[2 * pp] = lo2[0];
+      b0[2 * pp + 1] = lo2[1];
+      b1[2 * pp] = hi2[0];
+      b1[2 * pp + 1] = hi2[1];
+    }
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt) {
+      acc[tt][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(r.a[tt], b0, acc[tt][0], 0, 0, 0);
+      acc[tt][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(r.a[tt], b1, acc[tt][1], 0, 0, 0);
+    }
+  };
+
+  for (int s = 0; s < nst; ++s) {
+    // stages issued after this one (all waves alike)
+    const int ahead = min(kDepth - 2, nst - 1 - s);
+    if (ahead >= 2) wait_vmcnt<2 * (kGroupWLoads + 1)>();
+    else if (ahead == 1) wait_vmcnt<kGroupWLoads + 1>();
+    else wait_vmcnt<0>();
+    // every wave's copies of stage s have landed, and every wave is done
+    // with stage s - 1, whose buffers the next issue refills
+    lds_barrier();
+    if (s + kDepth - 1 < nst) issue(s + kDepth - 1);
+    const uint8_t* wst = wring + (s % kDepth) * kGroupWStage;
+    const uint8_t* xst = xring + (s % kDepth) * G::kXStage;
+    const int t0 = lo + kSU * s;
+    const int kmax = min(kSU, hi - t0);
+    int kb = part_end - t0;  // units k < kb belong to the current part (a stage meets at most one boundary)
+    kb = kb <= 0 ? 0 : min(kmax, kb);
+    auto run_units = [&](int k_begin, int k_end) {
+#pragma unroll
+      for (int k0 = 0; k0 < kSU; k0 += 2) {
+        if (k0 >= k_begin && k0 + 2 <= k_end) {
+          UnitRegs r0, r1;
+          load_unit(r0, wst, xst, k0);
+          load_unit(r1, wst, xst, k0 + 1);
+          math_unit(r0);
+          math_unit(r1);
+        } else {
+#pragma unroll
+          for (int u = 0; u < 2; ++u)
+            if (k0 + u >= k_begin && k0 + u < k_end) {
+              UnitRegs r;
+              load_unit(r, wst, xst, k0 + u);
+              math_unit(r);
+            }
+        }
+      }
+    };
+    run_units(0, kb);
+    if (kb < kmax) {
+      flush();
+      ++gcur;
+      part_end = min(hi, part_end + U);
+      run_units(kb, kmax);
+    }
+  }
+  if (hi > lo) flush();  // the last part
+}
+
+constexpr size_t kGroupMaxLds = 156 * 1024;
+
+template <int NT, int kDepth>
+static hipError_t launch_groups_one(const GroupParams& P, int wgs, hipStream_t stream) {
+  const size_t lds = GroupGeom<NT>::template lds_bytes<kDepth>();
+  if (lds > kGroupMaxLds) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((int4_gemm_strip_groups_kernel<NT, kDepth>), dim3(wgs), dim3(kGroupWaves * 64), lds, stream, P);
+  return hipGetLastError();
+}
+
+int strip_groups_slot_bytes(int n) { return n <= 16 ? GroupGeom<1>::kSlotBytes : GroupGeom<2>::kSlotBytes; }
+
+hipError_t launch_gemm_strip_groups(const uint16_t* x, const uint8_t* w, float* y, int n, int k, int m, int wgs,
+                                    int depth, float* slots, uint32_t* status, hipStream_t stream) {
+  GroupParams P = {};
+  P.x = x; P.w = w; P.y = y; P.slots = slots; P.status = status;
+  P.n = n; P.k = k; P.m = m;
+  P.units = k / kUnitRows;
+  P.strips = m / kStripCols;
+  const int groups = (P.strips + kGroupWaves - 1) / kGroupWaves;
+  const int total = groups * P.units;
+  P.base = total / wgs;
+  P.rem = total % wgs;
+  P.y_vec8 = (reinterpret_cast<uintptr_t>(y) & 7) == 0 ? 1 : 0;
+  const bool deep = depth >= 3;
+  if (n <= 16) return deep ? launch_groups_one<1, 3>(P, wgs, stream) : launch_groups_one<1, 2>(P, wgs, stream);
+  return deep ? launch_groups_one<2, 3>(P, wgs, stream) : launch_groups_one<2, 2>(P, wgs, stream);
 }
 
 // Records of W[K][M] from row order to strip order: one thread per 16-byte

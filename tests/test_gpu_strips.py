@@ -2,8 +2,9 @@
 byte-level restatement, and the strip GEMM against the oracle (dequantize the
 row-order stream, float32 matmul) within 1e-3 of the output RMS -- every
 plan shape (one whole strip per workgroup, strips shared by several
-workgroups, ranges over several strips), N from 1 to 32 (8 rows per launch),
-every ring depth and forced workgroup counts -- plus determinism, GEMM(N)
+workgroups, ranges over several strips), N from 1 to 32 (the strip kernel
+up to 8 rows, the strip-group kernel beyond), every ring depth, wave count
+and forced workgroup counts -- plus determinism, GEMM(N)
 against stacked single-row products, and a workspace shared with the
 row-order kernels."""
 
@@ -102,18 +103,43 @@ def test_strip_gemm_forced_plans(K, M):
                     assert rel_err(y.cpu().numpy(), yref) <= TOL, (K, M, N, splits, depth, waves)
 
 
+@pytest.mark.parametrize("K,M", [(2048, 2048), (3072, 8192), (2048, 1056)])
+def test_strip_group_gemm_forced_plans(K, M):
+    """N > 8 runs the strip-group kernel (8 strips a group, one launch; 9..16
+    rows of matrices under 2^26 weights run as two strip-kernel launches, so
+    the two smaller shapes here reach the group kernel at N = 17 and 32):
+    workgroup counts that split groups anywhere, a partial last group (M/32
+    not a multiple of 8), both ring depths, one and two 16-row tiles."""
+    from moat_amd.dequant import batched_int4_matmul, records_to_strips
+    blob, wdq = problem(K, M, 13 + K + M)
+    strips = records_to_strips(torch.from_numpy(blob).cuda(), K, M)
+    groups = (M // 32 + 7) // 8
+    for N in (9, 16, 17, 32):
+        x = O.synthetic_activations(N, K, 70 + N)
+        yref = x.astype(np.float32) @ wdq
+        xd = torch.from_numpy(x).cuda()
+        for splits in (1, 2, 3, 7, 33, 100, 255, 256):
+            if splits > groups * (K // 32):
+                continue
+            for depth in (2, 3):
+                say(f"case: strip group gemm K={K} M={M} N={N} workgroups={splits} depth={depth}")
+                y = batched_int4_matmul(xd, strips, K, M, strip_order=True, splits=splits, batch=depth)
+                assert rel_err(y.cpu().numpy(), yref) <= TOL, (K, M, N, splits, depth)
+
+
 def test_strip_gemm_is_deterministic_and_equals_stacked_gemv():
     from moat_amd.dequant import batched_int4_matmul, records_to_strips
     K, M = 2048, 2048
     blob, _ = problem(K, M, 77)
     strips = records_to_strips(torch.from_numpy(blob).cuda(), K, M)
-    x = torch.from_numpy(O.synthetic_activations(8, K, 78)).cuda()
-    say("case: strip gemm determinism and stacked GEMVs")
-    ref = batched_int4_matmul(x, strips, K, M, strip_order=True)
-    for _ in range(20):
-        assert torch.equal(batched_int4_matmul(x, strips, K, M, strip_order=True), ref)
-    rows = torch.cat([batched_int4_matmul(x[i:i + 1], strips, K, M, strip_order=True) for i in range(8)])
-    assert rel_err(ref.cpu().numpy(), rows.cpu().numpy()) <= TOL
+    for N in (8, 32):
+        x = torch.from_numpy(O.synthetic_activations(N, K, 78 + N)).cuda()
+        say(f"case: strip gemm determinism and stacked GEMVs N={N}")
+        ref = batched_int4_matmul(x, strips, K, M, strip_order=True)
+        for _ in range(20):
+            assert torch.equal(batched_int4_matmul(x, strips, K, M, strip_order=True), ref)
+        rows = torch.cat([batched_int4_matmul(x[i:i + 1], strips, K, M, strip_order=True) for i in range(N)])
+        assert rel_err(ref.cpu().numpy(), rows.cpu().numpy()) <= TOL
 
 
 def test_strip_gemm_shares_the_workspace_with_row_order_calls():
@@ -128,12 +154,16 @@ def test_strip_gemm_shares_the_workspace_with_row_order_calls():
         yref = x.astype(np.float32) @ wdq
         xd = torch.from_numpy(x).cuda()
         for rep in range(3):
-            for kind in ("strips", "records", "strips64", "general", "strips"):
+            for kind in ("strips", "records", "groups", "strips64", "general", "groups64", "strips"):
                 say(f"case: shared workspace N={N} rep={rep} {kind}")
                 if kind == "strips":
                     y = batched_int4_matmul(xd, strips, K, M, strip_order=True)
                 elif kind == "strips64":
                     y = batched_int4_matmul(xd, strips, K, M, strip_order=True, splits=64)
+                elif kind in ("groups", "groups64"):  # 16 rows (the strip-group kernel), first N compared
+                    x16 = torch.cat([xd, xd.new_zeros((16 - N, K))]) if N < 16 else xd
+                    y = batched_int4_matmul(x16, strips, K, M, strip_order=True,
+                                            splits=64 if kind == "groups64" else 0)[:N]
                 elif kind == "records":
                     y = batched_int4_matmul(xd, blob_d, K, M, algo=L.GEMM_MFMA, splits=8, front=L.FRONT_RECORDS)
                 else:
