@@ -219,6 +219,11 @@ int32_t moat_int4_gemm_tiles(const uint16_t* x_f16, const uint8_t* tiles, float*
  */
 int32_t moat_int4_records_to_strips(const uint8_t* superblocks, int32_t k, int32_t m, uint8_t* strips,
                                     hipStream_t stream);
+/* Strip order -> row order (the inverse of moat_int4_records_to_strips; same
+ * preconditions).  No counterpart in the reference: it restores the stream a
+ * row-order consumer (dequantize, moat_int4_gemm) reads. */
+int32_t moat_int4_strips_to_records(const uint8_t* strips, int32_t k, int32_t m, uint8_t* superblocks,
+                                    hipStream_t stream);
 int64_t moat_int4_gemm_strips_workspace_size(int32_t n, int32_t k, int32_t m,
                                              const moat_int4_gemm_options* options);
 int32_t moat_int4_gemm_strips(const uint16_t* x_f16, const uint8_t* strips, float* y_f32,
@@ -352,6 +357,12 @@ int32_t moat_int4_lut_gather(const int64_t* q, int64_t n, int32_t index_mode,
 /* *flag_out = 1 if any q[i] < 0 else 0 (int32 on the device); the branch test
  * of src/dequant.py:90. */
 int32_t moat_int4_any_negative(const int64_t* q, int64_t n, int32_t* flag_out, hipStream_t stream);
+
+/* out[i] = fp16(f32(q[i]) / divisor), float32 division then one rounding to
+ * fp16: numpy's float16 division of int8 values cast to float16 by a float16
+ * scalar -- the int8 fallback of antigravity-engine/src/model_loader.py:247
+ * (divisor 7).  divisor finite and non-zero. */
+int32_t moat_int4_i8_div_to_f16(const int8_t* q, int64_t n, float divisor, uint16_t* out_f16, hipStream_t stream);
 
 /* Round F32 or F64 values to fp16, nearest-even, one rounding (numpy's astype(float16)). */
 int32_t moat_int4_to_f16(const void* src, int32_t src_dtype, int64_t n, uint16_t* out_f16,

@@ -20,6 +20,7 @@ hipError_t launch_lut_gather(const int64_t* q, int64_t n, int index_mode, const 
                              int lut_len, uint16_t* out, hipStream_t st);
 hipError_t launch_any_negative(const int64_t* q, int64_t n, int32_t* flag, hipStream_t st);
 hipError_t launch_to_f16(const void* src, int src_dtype, int64_t n, uint16_t* out, hipStream_t st);
+hipError_t launch_i8_div_to_f16(const int8_t* q, int64_t n, float divisor, uint16_t* out, hipStream_t st);
 hipError_t launch_clear(void* p, int64_t bytes, hipStream_t st);
 hipError_t launch_quantize(const void* w, int dtype, int64_t n, int gsize, int scale_mode, int8_t* q,
                            uint16_t* scales, hipStream_t st);
@@ -52,6 +53,7 @@ hipError_t launch_stream_read(const void* src, int64_t bytes, uint32_t* sink, in
 hipError_t launch_gemm_strips(const uint16_t* x, const uint8_t* w, float* y, int n, int k, int m, int wgs, int depth,
                               int waves, float* slots, uint32_t* status, hipStream_t stream);
 hipError_t launch_records_to_strips(const uint8_t* sb, int k, int m, uint8_t* strips, hipStream_t stream);
+hipError_t launch_strips_to_records(const uint8_t* strips, int k, int m, uint8_t* sb, hipStream_t stream);
 int strips_waves(int n, int waves);
 int strips_depth(int n, int waves, int depth);
 hipError_t launch_gemm_strip_groups(const uint16_t* x, const uint8_t* w, float* y, int n, int k, int m, int wgs,
@@ -539,6 +541,17 @@ int32_t moat_int4_records_to_strips(const uint8_t* superblocks, int32_t k, int32
   return status_of(moat::launch_records_to_strips(superblocks, k, m, strips, stream));
 }
 
+int32_t moat_int4_strips_to_records(const uint8_t* strips, int32_t k, int32_t m, uint8_t* superblocks,
+                                    hipStream_t stream) {
+  if (k < 8 || (k % 8) != 0 || m < 32 || (m % 32) != 0) return MOAT_ERR_INVALID;
+  if ((int64_t)k * (m / 32) > ((int64_t)1 << 40)) return MOAT_ERR_INVALID;
+  if (!superblocks || !strips || !aligned(superblocks, 16) || !aligned(strips, 16)) return MOAT_ERR_INVALID;
+  const int64_t bytes = (int64_t)k * m / 256 * 144;
+  const uintptr_t a = reinterpret_cast<uintptr_t>(superblocks), b = reinterpret_cast<uintptr_t>(strips);
+  if (a < b + (uintptr_t)bytes && b < a + (uintptr_t)bytes) return MOAT_ERR_INVALID;  // the copies overlap
+  return status_of(moat::launch_strips_to_records(strips, k, m, superblocks, stream));
+}
+
 int64_t moat_int4_gemm_strips_workspace_size(int32_t n, int32_t k, int32_t m,
                                              const moat_int4_gemm_options* options) {
   if (!strips_shape_ok(n, k, m) || !strip_options_ok(options)) return -1;
@@ -739,6 +752,13 @@ int32_t moat_int4_to_f16(const void* src, int32_t src_dtype, int64_t n, uint16_t
   if (!src || !out_f16) return MOAT_ERR_INVALID;
   if (!aligned(src, src_dtype == MOAT_DTYPE_F64 ? 8 : 4) || !aligned(out_f16, 2)) return MOAT_ERR_INVALID;
   return status_of(moat::launch_to_f16(src, src_dtype, n, out_f16, stream));
+}
+
+int32_t moat_int4_i8_div_to_f16(const int8_t* q, int64_t n, float divisor, uint16_t* out_f16, hipStream_t stream) {
+  if (n < 0 || !(divisor == divisor) || divisor == 0.0f) return MOAT_ERR_INVALID;
+  if (n == 0) return MOAT_OK;
+  if (!q || !out_f16 || !aligned(out_f16, 2)) return MOAT_ERR_INVALID;
+  return status_of(moat::launch_i8_div_to_f16(q, n, divisor, out_f16, stream));
 }
 
 // ---- token sampling ----

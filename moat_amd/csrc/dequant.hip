@@ -236,6 +236,23 @@ hipError_t launch_any_negative(const int64_t* q, int64_t n, int32_t* flag, hipSt
   return hipGetLastError();
 }
 
+// fp16(f32(q) / divisor): numpy's float16 division of an int8 tensor cast to
+// float16 (exact) by a float16 scalar, which divides in float32 (correctly
+// rounded) and rounds the quotient to float16.
+__global__ void __launch_bounds__(256) i8_div_to_f16_kernel(const int8_t* __restrict__ q, int64_t n, float divisor,
+                                                            uint16_t* __restrict__ out) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const _Float16 h = (_Float16)((float)q[i] / divisor);
+    out[i] = __builtin_bit_cast(uint16_t, h);
+  }
+}
+
+hipError_t launch_i8_div_to_f16(const int8_t* q, int64_t n, float divisor, uint16_t* out, hipStream_t st) {
+  hipLaunchKernelGGL(i8_div_to_f16_kernel, dim3(grid_for(n)), dim3(256), 0, st, q, n, divisor, out);
+  return hipGetLastError();
+}
+
 hipError_t launch_to_f16(const void* src, int src_dtype, int64_t n, uint16_t* out, hipStream_t st) {
   hipLaunchKernelGGL(to_f16_kernel, dim3(grid_for(n)), dim3(256), 0, st, src, src_dtype, n, out);
   return hipGetLastError();

@@ -956,6 +956,51 @@ __global__ void records_to_strips_kernel(const uint8_t* __restrict__ src, int64_
   }
 }
 
+// Strip order back to row order: one thread per 16-byte chunk of the output
+// (row-order record R: chunk 0 = the scales of flat groups 8R .. 8R+7, chunk
+// c = 1..8 = the 16 payload bytes of flat group 8R + c - 1), each byte
+// gathered from its strip record.
+__global__ void strips_to_records_kernel(const uint8_t* __restrict__ strips, int64_t k, int64_t m,
+                                         uint4* __restrict__ dst) {
+  const int64_t gpr = m / kStripCols, blocks = k / 8;  // groups per row, records per strip
+  const int64_t chunks = (k * gpr / 8) * 9;
+  for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < chunks; e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t rec = e / 9, c = e - rec * 9;
+    if (c == 0) {
+      uint32_t h[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        uint32_t two[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const int64_t f = 8 * rec + 2 * i + t, r = f / gpr, g = f - r * gpr;
+          const uint8_t* sr = strips + (g * blocks + r / 8) * 144;
+          two[t] = *reinterpret_cast<const uint16_t*>(sr + 2 * (r % 8));
+        }
+        h[i] = two[0] | (two[1] << 16);
+      }
+      dst[e] = uint4{h[0], h[1], h[2], h[3]};
+    } else {
+      const int64_t f = 8 * rec + c - 1, r = f / gpr, g = f - r * gpr;
+      const uint8_t* sr = strips + (g * blocks + r / 8) * 144 + 16 + strip_row_pos((int)(r % 8));
+      uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int jb = 0; jb < 16; ++jb) w[jb >> 2] |= (uint32_t)sr[8 * jb] << (8 * (jb & 3));
+      dst[e] = uint4{w[0], w[1], w[2], w[3]};
+    }
+  }
+}
+
+hipError_t launch_strips_to_records(const uint8_t* strips, int k, int m, uint8_t* sb, hipStream_t stream) {
+  const int64_t chunks = ((int64_t)k * (m / kStripCols) / 8) * 9;
+  if (chunks == 0) return hipSuccess;
+  int64_t blocks = (chunks + 255) / 256;
+  if (blocks > 8192) blocks = 8192;
+  hipLaunchKernelGGL(strips_to_records_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, strips, (int64_t)k,
+                     (int64_t)m, reinterpret_cast<uint4*>(sb));
+  return hipGetLastError();
+}
+
 hipError_t launch_records_to_strips(const uint8_t* sb, int k, int m, uint8_t* strips, hipStream_t stream) {
   const int64_t chunks = (int64_t)(m / kStripCols) * (k / 8) * 9;
   if (chunks == 0) return hipSuccess;

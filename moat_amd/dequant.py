@@ -324,11 +324,12 @@ def records_to_strips(superblocks, K: int, M: int) -> torch.Tensor:
     """The quantized weights of a row-major K x M stream (``K % 8 == 0``,
     ``M % 32 == 0``) in strip order: strip g = columns 32g..32g+31, strips in
     column order, and inside a strip one 144-byte record per 8 rows (their 8
-    scales of the strip's group, then their 8 16-byte payloads).  A GPU uint8
-    tensor, read by :func:`batched_int4_matmul` with ``strip_order=True``
-    (``K >= 2048``): every workgroup streams one contiguous range of it.  (A
-    storage order with no counterpart in the reference, whose stream is the
-    row order; the q values and scales are unchanged.)"""
+    scales of the strip's group, then the 16 payload bytes of each column
+    pair for rows 0 2 1 3 4 6 5 7).  A GPU uint8 tensor, read by
+    :func:`batched_int4_matmul` with ``strip_order=True`` (``K >= 2048``):
+    every workgroup streams one contiguous range of it.  (A storage order
+    with no counterpart in the reference, whose stream is the row order; the
+    q values and scales are unchanged.)"""
     K, M = int(K), int(M)
     if K < 8 or K % 8 != 0 or M < 32 or M % 32 != 0:
         raise ValueError(f"strip order needs K % 8 == 0 and M % 32 == 0 (got K={K}, M={M})")
@@ -338,6 +339,51 @@ def records_to_strips(superblocks, K: int, M: int) -> torch.Tensor:
     _lib.check(_lib.load().moat_int4_records_to_strips(D.ptr(blob), K, M, D.ptr(strips), D.stream()),
                "records_to_strips")
     return strips
+
+
+def strips_to_records(strips, K: int, M: int) -> torch.Tensor:
+    """Row-order records (``uint8[K*M/256, 144]`` on the GPU) from a strip-order
+    stream: the inverse of :func:`records_to_strips`."""
+    K, M = int(K), int(M)
+    if K < 8 or K % 8 != 0 or M < 32 or M % 32 != 0:
+        raise ValueError(f"strip order needs K % 8 == 0 and M % 32 == 0 (got K={K}, M={M})")
+    n_sb = K * M // SUPERBLOCK_ELEMS
+    blob = _blob_to_device(strips, n_sb)
+    out = torch.empty((n_sb, SUPERBLOCK_BYTES), dtype=torch.uint8, device=blob.device)
+    _lib.check(_lib.load().moat_int4_strips_to_records(D.ptr(blob), K, M, D.ptr(out), D.stream()),
+               "strips_to_records")
+    return out
+
+
+def to_f16(t) -> torch.Tensor:
+    """A GPU fp16 tensor of the same shape: fp16 as is; fp32 and fp64 rounded
+    once, nearest-even (numpy's ``astype(float16)``; a device float64 ->
+    float32 -> float16 chain would round twice); bf16 through float32 (exact);
+    integers and bools through float64 (exact below 2^53)."""
+    t = D.to_device(t)
+    if t.dtype == torch.float16:
+        return t
+    if t.dtype not in (torch.float32, torch.float64):
+        t = t.to(torch.float32 if t.dtype == torch.bfloat16 else torch.float64)
+    t = t.contiguous()
+    code = _lib.DTYPE_F64 if t.dtype == torch.float64 else _lib.DTYPE_F32
+    out = torch.empty(t.shape, dtype=torch.float16, device=t.device)
+    _lib.check(_lib.load().moat_int4_to_f16(D.ptr(t), code, t.numel(), D.ptr(out), D.stream()), "to_f16")
+    return out
+
+
+def i8_div_to_f16(q, divisor: float) -> torch.Tensor:
+    """``fp16(f32(q) / divisor)`` for int8 ``q``: numpy's float16 division of
+    ``q.astype(float16) / divisor`` (one float32 division, then one rounding
+    to float16), on the GPU."""
+    t = D.to_device(q)
+    if t.dtype != torch.int8:
+        raise ValueError("i8_div_to_f16 takes int8 values")
+    t = t.contiguous()
+    out = torch.empty(t.shape, dtype=torch.float16, device=t.device)
+    _lib.check(_lib.load().moat_int4_i8_div_to_f16(D.ptr(t), t.numel(), float(divisor), D.ptr(out), D.stream()),
+               "i8_div_to_f16")
+    return out
 
 
 def _fused_inputs(x, K: int, M: int, blobs):

@@ -21,7 +21,19 @@ GPU counterpart of ``antigravity-engine/src/model_loader.py``:
   :class:`QuantizedSuperBlockTensor` and :class:`MemoryBudgetValidator`: the
   reference's helpers (``:281-403``) with the records on the GPU.
 * :func:`save_superblocks` / :func:`load_superblocks`: a record file (magic,
-  original shape, then the records as written) so that quantization runs once.
+  original shape, layout, then the records as written) so that quantization
+  runs once.
+
+Storage order.  A 2-D weight ``W[K][M]`` that the strip GEMM can read (K >=
+2048, K % 32 == 0, M % 32 == 0) is stored in strip order by default (the
+loader's ``layout="auto"``; :func:`moat_amd.dequant.records_to_strips`): the
+order the batched decode GEMM streams fastest.  Every other tensor, or
+``layout="row"``, keeps the reference's row order.  The layer dict says which
+(``'layout'``); :meth:`ModelWeightLoader.row_records` gives row order either
+way.
+
+Rounding.  Float inputs are rounded to fp16 once, nearest-even, by a library
+kernel (numpy's ``astype(float16)``), float64 included.
 """
 
 from __future__ import annotations
@@ -34,35 +46,78 @@ import numpy as np
 import torch
 
 from . import _device as D
-from .dequant import GROUP_SIZE, SUPERBLOCK_BYTES, SUPERBLOCK_ELEMS, quantize_to_superblocks, unpack_superblock_weights
-from .engine_dequant import quantize_weights_int4
+from .dequant import (GROUP_SIZE, SUPERBLOCK_BYTES, SUPERBLOCK_ELEMS, i8_div_to_f16, quantize_to_superblocks,
+                      records_to_strips, strips_to_records, to_f16, unpack_superblock_weights)
 
 IOS_APP_MEMORY_CEILING_BYTES = 4500 * 1024 * 1024  # model_loader.py:21
 MODEL_WEIGHT_BUDGET_BYTES = 2500 * 1024 * 1024  # model_loader.py:22, the loader's default budget
-RECORD_FILE_MAGIC = b"MOATI4R1"
+RECORD_FILE_MAGIC = b"MOATI4R2"      # with a layout byte
+RECORD_FILE_MAGIC_V1 = b"MOATI4R1"   # row order, no layout byte (still read)
+LAYOUTS = ("row", "strip")
+
+
+def strip_layout_ok(shape) -> bool:
+    """Whether the strip GEMM can read a weight of this shape: 2-D ``(K, M)``
+    with K >= 2048, K % 32 == 0 and M % 32 == 0."""
+    return len(shape) == 2 and shape[0] >= 2048 and shape[0] % 32 == 0 and shape[1] % 32 == 0
+
+
+def _codes_from_records(records: torch.Tensor):
+    """int8 codes (q, one per element, in [-8, 7]) and fp16 scales (one per 32
+    elements) of a row-order record stream: the quantizer's output read back
+    from the records it wrote (low nibble = element 2j, high = 2j+1, each
+    stored as q + 8)."""
+    rec = records.reshape(-1, SUPERBLOCK_BYTES)
+    scales = rec[:, :16].contiguous().view(torch.float16).reshape(-1)
+    pay = rec[:, 16:].reshape(-1)
+    lo = (pay & 15).to(torch.int8) - 8
+    hi = (pay >> 4).to(torch.int8) - 8
+    q = torch.stack([lo, hi], dim=1).reshape(-1)
+    return q, scales
 
 
 class ModelWeightLoader:
     """Loads weight tensors as INT4 records on the GPU (``model_loader.py:33-134``)."""
 
-    def __init__(self, memory_budget_bytes: int = MODEL_WEIGHT_BUDGET_BYTES):
+    def __init__(self, memory_budget_bytes: int = MODEL_WEIGHT_BUDGET_BYTES, layout: str = "auto"):
+        if layout not in ("auto",) + LAYOUTS:
+            raise ValueError(f"layout must be 'auto', 'row' or 'strip' (got {layout!r})")
         self.memory_budget_bytes = memory_budget_bytes
+        self.layout = layout
         self.layers: Dict[str, Dict] = {}
         self.total_loaded_bytes = 0
         self._host_io = set()
 
     def load_and_repack_layer(self, layer_name: str, weights_fp16, group_size: int = 32,
-                              keep_q: bool = True) -> Dict:
+                              keep_q: bool = True, layout: Optional[str] = None) -> Dict:
         """Quantize and pack one weight tensor (any shape, any float dtype,
         numpy or torch).  Returns ``layer_name``, ``original_shape``,
         ``n_elements`` (before padding), ``superblocks`` (device ``uint8[S,
-        144]``), ``memory_bytes`` (S * 144) and, with ``keep_q``, the int8
-        codes ``q_weights`` and fp16 ``scales`` of the padded tensor (as numpy
-        arrays, like the reference)."""
+        144]``, in ``layout`` order), ``layout`` (``'row'`` or ``'strip'``),
+        ``memory_bytes`` (S * 144) and, with ``keep_q``, the int8 codes
+        ``q_weights`` and fp16 ``scales`` of the padded tensor in row order
+        (numpy arrays, like the reference), read back from the records rather
+        than quantized a second time.
+
+        ``group_size``: the reference's parameter; the 144-byte record holds
+        groups of 32 weights, so 32 is the only value (ValueError otherwise).
+        ``layout``: ``'auto'`` (the loader's default: strip order when
+        :func:`strip_layout_ok`), ``'row'``, or ``'strip'`` (2-D with K % 8 == 0
+        and M % 32 == 0, else ValueError)."""
         if group_size != 32:
             raise ValueError("the 144-byte records hold groups of 32 weights (group_size=32)")
+        layout = layout or self.layout
+        if layout not in ("auto",) + LAYOUTS:
+            raise ValueError(f"layout must be 'auto', 'row' or 'strip' (got {layout!r})")
         original_shape = tuple(weights_fp16.shape)
-        w = D.to_device(weights_fp16).reshape(-1).to(torch.float16)  # round to nearest even, as astype
+        if layout == "strip" and not (len(original_shape) == 2 and original_shape[0] % 8 == 0
+                                      and original_shape[0] > 0 and original_shape[1] % 32 == 0
+                                      and original_shape[1] > 0):
+            raise ValueError(f"strip order needs a 2-D (K, M) weight with K % 8 == 0 and M % 32 == 0 "
+                             f"(got {original_shape})")
+        if layout == "auto":
+            layout = "strip" if strip_layout_ok(original_shape) else "row"
+        w = to_f16(weights_fp16).reshape(-1)  # one nearest-even rounding, as astype
         n_elements = w.numel()
         rem = n_elements % SUPERBLOCK_ELEMS
         if rem:
@@ -75,6 +130,9 @@ class ModelWeightLoader:
                 f"memory budget of {self.memory_budget_bytes / 1e9:.2f} GB. "
                 f"Currently loaded: {self.total_loaded_bytes / 1e9:.2f} GB.")
         records = quantize_to_superblocks(w, scale_rule="f16")
+        q_codes = _codes_from_records(records) if keep_q else None
+        if layout == "strip":
+            records = records_to_strips(records, original_shape[0], original_shape[1]).reshape(n_sb, SUPERBLOCK_BYTES)
         if D.is_tensor(weights_fp16) and weights_fp16.is_cuda:
             self._host_io.discard(layer_name)
         else:
@@ -84,12 +142,12 @@ class ModelWeightLoader:
             "original_shape": original_shape,
             "n_elements": n_elements,
             "superblocks": records,
+            "layout": layout,
             "memory_bytes": layer_memory_bytes,
         }
         if keep_q:
-            q, s = quantize_weights_int4(w)
-            layer["q_weights"] = D.to_host(q)
-            layer["scales"] = D.to_host(s)
+            layer["q_weights"] = D.to_host(q_codes[0])
+            layer["scales"] = D.to_host(q_codes[1])
         self.layers[layer_name] = layer
         self.total_loaded_bytes += layer_memory_bytes
         return layer
@@ -102,9 +160,21 @@ class ModelWeightLoader:
         if layer_name not in self.layers:
             raise KeyError(f"Layer '{layer_name}' not found in loader")
         layer = self.layers[layer_name]
-        flat = unpack_superblock_weights(layer["superblocks"], layer["superblocks"].shape[0])
+        rows = self.row_records(layer_name)
+        flat = unpack_superblock_weights(rows, rows.shape[0])
         out = flat[: layer["n_elements"]].reshape(layer["original_shape"])
         return D.to_host(out) if layer_name in self._host_io else out
+
+    def row_records(self, layer_name: str) -> torch.Tensor:
+        """The layer's records in row order (the stored stream itself when the
+        layer is in row order)."""
+        if layer_name not in self.layers:
+            raise KeyError(f"Layer '{layer_name}' not found in loader")
+        layer = self.layers[layer_name]
+        if layer.get("layout", "row") == "strip":
+            K, M = layer["original_shape"]
+            return strips_to_records(layer["superblocks"], K, M)
+        return layer["superblocks"]
 
     def unload_layer(self, layer_name: str) -> None:
         """Drop a layer (its records are freed with the last reference) and
@@ -134,7 +204,8 @@ class ModelWeightLoader:
         (``model_loader.py:217-251``): F32 (type 0) is rounded to fp16 on the
         GPU, F16 (type 1) is taken as stored, and any other type is read as
         one int8 per element (zero-filled past the end of the file) and
-        mapped to fp16(int8 / 7), as the reference does.  The shape is the
+        mapped to fp16(int8 / 7) as the reference's numpy float16 division
+        computes it (library kernels for both conversions).  The shape is the
         dims in stored order.  Returns the parsed header."""
         if not os.path.exists(gguf_path):
             raise FileNotFoundError(f"GGUF model file not found at '{gguf_path}'. Please provide a valid file path.")
@@ -148,17 +219,13 @@ class ModelWeightLoader:
                 f.seek(base + t["offset"])
                 if t["type"] == 0:
                     host = np.frombuffer(f.read(4 * n), dtype=np.float32)
-                    w = torch.from_numpy(host.copy()).to(dev).to(torch.float16)
+                    w = to_f16(torch.from_numpy(host.copy()).to(dev))
                 elif t["type"] == 1:
                     w = torch.from_numpy(np.frombuffer(f.read(2 * n), dtype=np.float16).copy()).to(dev)
                 else:
                     raw = f.read(n)
                     raw = raw + b"\x00" * (n - len(raw))
-                    q = torch.from_numpy(np.frombuffer(raw, dtype=np.int8).copy()).to(dev)
-                    # int8 -> fp16 is exact; the quotient by 7 in fp32 (correctly
-                    # rounded elementwise division), then one rounding to fp16
-                    seven = torch.full_like(q, 7, dtype=torch.float32)
-                    w = (q.to(torch.float32) / seven).to(torch.float16)
+                    w = i8_div_to_f16(torch.from_numpy(np.frombuffer(raw, dtype=np.int8).copy()).to(dev), 7.0)
                 self.load_and_repack_layer(name, w.reshape(shape))
         return info
 
@@ -288,7 +355,7 @@ class SuperBlockRepacker:
         if group_size != GROUP_SIZE or groups_per_superblock != SUPERBLOCK_ELEMS // GROUP_SIZE:
             raise ValueError("the 144-byte records hold 8 groups of 32 weights")
         shape = tuple(matrix.shape)
-        w = D.to_device(matrix).reshape(-1).to(torch.float16)
+        w = to_f16(matrix).reshape(-1)  # one nearest-even rounding, as astype
         rem = w.numel() % SUPERBLOCK_ELEMS
         if rem:
             w = torch.cat([w, torch.zeros(SUPERBLOCK_ELEMS - rem, dtype=torch.float16, device=w.device)])
@@ -351,9 +418,12 @@ class SafetensorsWeightReader:
 GGUFWeightReader = SafetensorsWeightReader  # model_loader.py:341, the same reader under the GGUF name
 
 
-def save_superblocks(path: str, records, original_shape: Tuple[int, ...]) -> None:
+def save_superblocks(path: str, records, original_shape: Tuple[int, ...], layout: str = "row") -> None:
     """Write a record file: 8-byte magic, uint32 rank, rank x uint64 dims,
-    uint64 record count, then the records as stored (144 bytes each)."""
+    uint64 record count, one layout byte (0 row order, 1 strip order), then
+    the records as stored (144 bytes each)."""
+    if layout not in LAYOUTS:
+        raise ValueError(f"layout must be 'row' or 'strip' (got {layout!r})")
     data = D.to_host(records) if D.is_tensor(records) else np.asarray(records)
     data = np.ascontiguousarray(data, dtype=np.uint8).reshape(-1)
     if data.size % SUPERBLOCK_BYTES:
@@ -367,20 +437,31 @@ def save_superblocks(path: str, records, original_shape: Tuple[int, ...]) -> Non
         f.write(struct.pack("<I", len(dims)))
         f.write(struct.pack(f"<{len(dims)}Q", *dims))
         f.write(struct.pack("<Q", n_sb))
+        f.write(struct.pack("<B", LAYOUTS.index(layout)))
         f.write(data.tobytes())
 
 
-def load_superblocks(path: str, device: bool = False):
-    """Read a record file: (records ``uint8[S, 144]``, original shape); the
-    records on the GPU when ``device`` is true."""
+def load_superblocks(path: str, device: bool = False, with_layout: bool = False):
+    """Read a record file: (records ``uint8[S, 144]``, original shape), plus the
+    layout (``'row'`` or ``'strip'``) when ``with_layout``; the records on the
+    GPU when ``device`` is true.  Files of the first version (no layout
+    byte) are row order."""
     with open(path, "rb") as f:
-        if f.read(8) != RECORD_FILE_MAGIC:
+        magic = f.read(8)
+        if magic not in (RECORD_FILE_MAGIC, RECORD_FILE_MAGIC_V1):
             raise ValueError(f"{path} is not a record file")
         (rank,) = struct.unpack("<I", f.read(4))
         dims = struct.unpack(f"<{rank}Q", f.read(8 * rank))
         (n_sb,) = struct.unpack("<Q", f.read(8))
+        layout = "row"
+        if magic == RECORD_FILE_MAGIC:
+            (code,) = struct.unpack("<B", f.read(1))
+            if code >= len(LAYOUTS):
+                raise ValueError(f"{path}: unknown layout code {code}")
+            layout = LAYOUTS[code]
         data = np.frombuffer(f.read(n_sb * SUPERBLOCK_BYTES), dtype=np.uint8)
     if data.size != n_sb * SUPERBLOCK_BYTES:
         raise ValueError(f"{path}: truncated record file")
     records = data.reshape(n_sb, SUPERBLOCK_BYTES).copy()
-    return (D.to_device(records) if device else records), tuple(int(d) for d in dims)
+    out = (D.to_device(records) if device else records), tuple(int(d) for d in dims)
+    return out + (layout,) if with_layout else out

@@ -24,13 +24,26 @@ def _oracle_layer(w):
 
 
 def test_record_file_round_trip(tmp_path):
-    from moat_amd.loader import load_superblocks, save_superblocks
+    import struct
+    from moat_amd.loader import RECORD_FILE_MAGIC_V1, load_superblocks, save_superblocks
     w = O.synthetic_weights(64, 96, 0.02, 5)
     blob = O.quantize_pack_a(w).reshape(-1, 144)
     path = os.path.join(tmp_path, "layer.i4r")
     save_superblocks(path, blob, (64, 96))
     got, shape = load_superblocks(path)
     assert shape == (64, 96) and got.shape == blob.shape and np.array_equal(got, blob)
+    strips = O.records_to_strips(blob.reshape(-1), 64, 96).reshape(-1, 144)
+    save_superblocks(path, strips, (64, 96), layout="strip")
+    got, shape, layout = load_superblocks(path, with_layout=True)
+    assert layout == "strip" and shape == (64, 96) and np.array_equal(got, strips)
+    with pytest.raises(ValueError):
+        save_superblocks(path, blob, (64, 96), layout="tiles")
+    # a file of the first version (no layout byte) reads as row order
+    with open(path, "wb") as f:
+        f.write(RECORD_FILE_MAGIC_V1 + struct.pack("<I", 2) + struct.pack("<2Q", 64, 96)
+                + struct.pack("<Q", blob.shape[0]) + blob.tobytes())
+    got, shape, layout = load_superblocks(path, with_layout=True)
+    assert layout == "row" and np.array_equal(got, blob)
     with open(path, "r+b") as f:
         f.write(b"NOTMOAT!")
     with pytest.raises(ValueError):
@@ -61,9 +74,12 @@ def test_safetensors_reader_rounds_to_fp16(tmp_path):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("shape", [(256, 512), (100, 30), (2048, 2048)])
+@pytest.mark.parametrize("shape", [(256, 512), (100, 30), (2048, 2048), (3072, 256)])
 def test_gpu_loader_matches_oracle(shape):
-    from moat_amd.loader import ModelWeightLoader
+    """Row order for shapes the strip GEMM cannot read, strip order (the
+    oracle's regrouping of the same records) for those it can; codes and
+    scales read back from the records equal the quantizer's."""
+    from moat_amd.loader import ModelWeightLoader, strip_layout_ok
     print(f"case: loader shape={shape}", flush=True)
     w = O.synthetic_weights(int(np.prod(shape)), 1, 0.02, 11).reshape(shape)
     q, s, records, _ = _oracle_layer(w)
@@ -71,13 +87,89 @@ def test_gpu_loader_matches_oracle(shape):
     layer = loader.load_and_repack_layer("x", w)
     assert layer["original_shape"] == shape and layer["n_elements"] == int(np.prod(shape))
     assert layer["memory_bytes"] == records.shape[0] * 144
-    assert np.array_equal(layer["superblocks"].cpu().numpy(), records)
+    if strip_layout_ok(shape):
+        assert layer["layout"] == "strip"
+        want = O.records_to_strips(records.reshape(-1), *shape).reshape(-1, 144)
+        assert np.array_equal(layer["superblocks"].cpu().numpy(), want)
+    else:
+        assert layer["layout"] == "row"
+        assert np.array_equal(layer["superblocks"].cpu().numpy(), records)
+    assert np.array_equal(loader.row_records("x").cpu().numpy(), records)
     assert np.array_equal(layer["q_weights"], q) and np.array_equal(layer["scales"].view(np.uint16), s.view(np.uint16))
     deq = loader.dequantize_layer("x")  # numpy in, numpy out
     assert isinstance(deq, np.ndarray)
     want = O.decode_superblocks(records, records.shape[0])[: int(np.prod(shape))].reshape(shape)
     assert deq.shape == shape and np.array_equal(deq.view(np.uint16), want.view(np.uint16))
     assert loader.total_loaded_bytes == records.shape[0] * 144
+
+
+@pytest.mark.gpu
+def test_gpu_loader_layout_choice_and_strip_round_trip():
+    """layout='row' keeps row order for a strip-eligible shape; layout='strip'
+    on a shape only the conversion accepts; the strip -> row kernel inverts
+    the row -> strip kernel; a bad layout is a ValueError."""
+    from moat_amd.dequant import records_to_strips, strips_to_records
+    from moat_amd.loader import ModelWeightLoader
+    print("case: loader layouts", flush=True)
+    w = O.synthetic_weights(2048 * 64, 1, 0.02, 21).reshape(2048, 64)
+    _, _, records, _ = _oracle_layer(w)
+    row = ModelWeightLoader(layout="row").load_and_repack_layer("x", w)
+    assert row["layout"] == "row" and np.array_equal(row["superblocks"].cpu().numpy(), records)
+    w2 = O.synthetic_weights(64 * 96, 1, 0.02, 22).reshape(64, 96)
+    _, _, rec2, _ = _oracle_layer(w2)
+    loader = ModelWeightLoader()
+    st = loader.load_and_repack_layer("y", w2, layout="strip")
+    assert st["layout"] == "strip"
+    assert np.array_equal(st["superblocks"].cpu().numpy().reshape(-1), O.records_to_strips(rec2.reshape(-1), 64, 96))
+    deq = loader.dequantize_layer("y")
+    want = O.decode_superblocks(rec2, rec2.shape[0]).reshape(64, 96)
+    assert np.array_equal(deq.view(np.uint16), want.view(np.uint16))
+    with pytest.raises(ValueError):
+        loader.load_and_repack_layer("z", np.zeros((60, 96), np.float16), layout="strip")
+    with pytest.raises(ValueError):
+        ModelWeightLoader(layout="tiles")
+    for K, M in ((8, 32), (40, 256), (2048, 5504)):
+        blob = O.quantize_pack_a(O.synthetic_weights(K, M, 0.02, K + M)).reshape(-1)
+        d = torch.from_numpy(blob).cuda()
+        back = strips_to_records(records_to_strips(d, K, M), K, M)
+        assert torch.equal(back.reshape(-1), d), (K, M)
+
+
+@pytest.mark.gpu
+def test_gpu_to_f16_rounds_once():
+    """float64 -> fp16 in one nearest-even rounding (numpy's astype): values
+    just above an fp16 midpoint whose even neighbour is below -- a float64 ->
+    float32 -> float16 chain lands on the midpoint and rounds down -- plus
+    float32, bfloat16 and integer inputs; and the loader packs the
+    single-rounded values."""
+    from moat_amd.dequant import to_f16
+    from moat_amd.loader import ModelWeightLoader
+    print("case: to_f16 rounding", flush=True)
+    rng = np.random.default_rng(31)
+    lo = (rng.integers(0, 1 << 15, 4096) & ~1).astype(np.uint16)  # even positive fp16 patterns
+    lo = lo[np.isfinite(lo.view(np.float16)) & (lo.view(np.float16) != np.float16(65504))]
+    a = lo.view(np.float16).astype(np.float64)
+    b = (lo + 1).view(np.float16).astype(np.float64)
+    mid = (a + b) / 2
+    v = mid + np.abs(b - a) * 2.0 ** -40  # above the midpoint, below a float32 half-ulp of it
+    want = v.astype(np.float16)  # numpy: one rounding
+    assert np.array_equal(want.view(np.uint16), (lo + 1))  # the single rounding goes up
+    v = np.concatenate([v, -v])  # and the same magnitudes negative
+    want = v.astype(np.float16)
+    got = to_f16(torch.from_numpy(v).cuda()).cpu().numpy()
+    assert np.array_equal(got.view(np.uint16), want.view(np.uint16))
+    chained = torch.from_numpy(v).to(torch.float32).to(torch.float16).numpy()
+    assert not np.array_equal(chained.view(np.uint16), want.view(np.uint16))  # what the chain would give
+    f32 = (rng.standard_normal(1000) * 3).astype(np.float32)
+    assert np.array_equal(to_f16(torch.from_numpy(f32).cuda()).cpu().numpy(), f32.astype(np.float16))
+    bf = torch.from_numpy(f32).to(torch.bfloat16)
+    assert np.array_equal(to_f16(bf.cuda()).cpu().numpy(), bf.to(torch.float32).numpy().astype(np.float16))
+    ints = np.arange(-3000, 3000, 7, dtype=np.int64)
+    assert np.array_equal(to_f16(torch.from_numpy(ints).cuda()).cpu().numpy(), ints.astype(np.float16))
+    w = np.resize(v, 256 * 8).reshape(8, 256) * 1e-3
+    _, _, records, _ = _oracle_layer(w)
+    layer = ModelWeightLoader().load_and_repack_layer("f64", w)
+    assert np.array_equal(layer["superblocks"].cpu().numpy(), records)
 
 
 @pytest.mark.gpu
@@ -99,9 +191,11 @@ def test_gpu_loader_budget_and_safetensors(tmp_path):
         _, _, records, _ = _oracle_layer(t.to(torch.float32).numpy())
         assert np.array_equal(layers[name]["superblocks"].cpu().numpy(), records), name
         rec_path = os.path.join(tmp_path, name + ".i4r")
-        save_superblocks(rec_path, layers[name]["superblocks"], layers[name]["original_shape"])
-        back, shape = load_superblocks(rec_path, device=True)
+        save_superblocks(rec_path, layers[name]["superblocks"], layers[name]["original_shape"],
+                         layout=layers[name]["layout"])
+        back, shape, layout = load_superblocks(rec_path, device=True, with_layout=True)
         assert shape == tuple(t.shape) and torch.equal(back, layers[name]["superblocks"])
+        assert layout == layers[name]["layout"]
 
 
 # ---------------------------------------------------------------------------
