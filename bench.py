@@ -350,6 +350,9 @@ def main() -> int:
                          "moat_int4_gemm_strips; needs K >= 2048")
     ap.add_argument("--fused", action="store_true",
                     help="layer_h2048: Q, K, V in one launch and gate/up fused with SwiGLU (h feeds down)")
+    ap.add_argument("--driver", action="store_true",
+                    help="layer_h2048: through moat_amd.layer.LayerProjections (strip order, Q|K|V and gate|up "
+                         "each one launch, SwiGLU kernel, one graph over consecutive layers)")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"), default=None,
                     help="no GPU run: turn two rocprofv3 --pmc counter CSVs (FETCH_SIZE, WRITE_SIZE) of "
                          "`bench.py --ns N` into profiles/traffic_<config>.json")
@@ -700,12 +703,144 @@ def run_quantize_load(args) -> int:
     return 0
 
 
+def run_layer_driver(args) -> int:
+    """One decoder layer's projections through moat_amd.layer.LayerProjections
+    at N = 16: Q|K|V in one strip-order launch, O, gate|up in one launch, the
+    SwiGLU kernel (fp16 h) and down(h), captured in one HIP graph that holds
+    `copies` distinct layers (>= 300 MB of records, so no layer is served from
+    the Infinity Cache), like consecutive layers of a model.  A step is one
+    layer."""
+    import torch
+    from moat_amd.dequant import quantize_to_superblocks
+    from moat_amd.layer import LayerProjections
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    N = int(args.ns.split(",")[0]) if args.ns else LAYER_N
+    names = {"q": "q_proj", "k": "k_proj", "v": "v_proj", "o": "o_proj", "gate": "gate_proj", "up": "up_proj",
+             "down": "down_proj"}
+    rng = np.random.default_rng(LAYER_SEED)
+    first = {}
+    for name, K, M in LAYER:
+        w = rng.standard_normal((K, M), dtype=np.float32) * np.float32(0.02)
+        first[names[name]] = (quantize_to_superblocks(torch.from_numpy(w).to(dev)), K, M)
+    layer_bytes = sum(144 * K * M // 256 for _, K, M in LAYER)
+    copies = max(2, -(-ROTATE_BYTES // layer_bytes))
+    log(f"[bench] layer driver: {layer_bytes / 1e6:.2f} MB of records per layer, {copies} layers, N={N}")
+    layers = [LayerProjections(first, max_batch=N)]
+    for c in range(1, copies):  # distinct weight memory per layer (same values)
+        layers.append(LayerProjections({k: (r.clone(), K, M) for k, (r, K, M) in first.items()}, max_batch=N))
+    log(f"[bench] layouts: {layers[0].layouts}")
+    xr = np.random.default_rng(2400)
+    for lay in layers:
+        for buf in (lay.x, lay.attn, lay.x_mlp):
+            buf.copy_(torch.from_numpy(xr.standard_normal(tuple(buf.shape), dtype=np.float32).astype(np.float16)))
+    cap = torch.cuda.Stream()
+    cap.wait_stream(torch.cuda.current_stream())
+
+    def graph_of(fn):
+        with torch.cuda.stream(cap):
+            for lay in layers[:2]:
+                fn(lay)
+        cap.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=cap):
+            for lay in layers:
+                fn(lay)
+        torch.cuda.synchronize()
+        return g
+
+    def timed(g, replays):
+        with torch.cuda.stream(cap):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(cap)
+            for _ in range(replays):
+                g.replay()
+            e1.record(cap)
+        e1.synchronize()
+        return e0.elapsed_time(e1) * 1e3  # us
+
+    graph = graph_of(lambda lay: lay.run(N))
+    warm_us = timed(graph, 1)
+    timed(graph, max(1, int(20000 / max(warm_us, 1.0))))
+    replays = max(1, -(-args.steps // copies))
+    us = timed(graph, replays) / (replays * copies)
+    value = N / (us / 1e6)
+    H, I = 2048, 5632
+    qkv_m = layers[0].q_dim + 2 * layers[0].kv_dim
+    parts = {
+        "qkv": (lambda lay: lay.attention_inputs(N), algo_bytes(N, H, qkv_m)),
+        "o": (lambda lay: lay.output_projection(N), algo_bytes(N, layers[0].q_dim, H)),
+        "gate_up+swiglu": (lambda lay: lay.mlp_front(N), algo_bytes(N, H, 2 * I) + 8 * N * I + 2 * N * I),
+        "down": (lambda lay: lay.down_projection(N), algo_bytes(N, I, H)),
+    }
+    bytes_layer = sum(b for _, b in parts.values())
+    log(f"[bench] layer driver: {us:.2f} us/layer, {value:.0f} tok/s, {bytes_layer / us / 1e3:.0f} GB/s")
+    per_part = {}
+    for pname, (fn, b) in parts.items():
+        g = graph_of(fn)
+        timed(g, 2)
+        reps = max(2, args.calls // copies)
+        pus = timed(g, reps) / (reps * copies)
+        per_part[pname] = {"us_per_call": round(pus, 3), "algorithmic_bytes": b, "gbs": round(b / pus / 1e3, 1),
+                           "roofline_frac": round(b / pus / 1e3 / HBM_PEAK_GBS, 4)}
+        log(f"[bench] {pname:15s}: {pus:7.2f} us  {b / pus / 1e3:6.0f} GB/s")
+        del g
+    for lay in layers:
+        lay.check()
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+        from oracle import superblock_oracle as O
+        hosts = {k: r.cpu().numpy() for k, (r, K, M) in first.items()}
+        x_h, a_h, m_h = (t[:N].cpu().numpy() for t in (layers[0].x, layers[0].attn, layers[0].x_mlp))
+        times = []
+        t_start = time.perf_counter()
+        while len(times) < 3 or (time.perf_counter() - t_start < args.cpu_budget and len(times) < 10):
+            t0 = time.perf_counter()
+            for k in ("q_proj", "k_proj", "v_proj"):
+                O.gemm_ref(x_h, hosts[k], H, H)
+            O.gemm_ref(a_h, hosts["o_proj"], H, H)
+            h = O.swiglu_ref(m_h, hosts["gate_proj"], hosts["up_proj"], H, I).astype(np.float16)
+            O.gemm_ref(h, hosts["down_proj"], I, H)
+            times.append(time.perf_counter() - t0)
+        med = float(np.median(times))
+        cpu = {"value": N / med, "unit": "tok/s", "cores": os.cpu_count(), "kind": "port",
+               "sample": (f"numpy oracle: one layer's projections (Q, K, V, O, SwiGLU of gate/up, down of fp16 h; "
+                          f"decode records, float32 matmul) at N={N}, median of {len(times)} layers; "
+                          f"host os.cpu_count()={os.cpu_count()}")}
+        log(f"[bench] CPU baseline: {cpu['value']:.1f} tok/s")
+
+    out = {
+        "metric": "INT4 dequant-GEMM µs/call, HBM GB/s (% roofline), tok/s at N=1..32",
+        "value": round(value, 1), "unit": "tok/s", "n_gpus": 1, "steps": replays * copies, "warmup": args.warmup,
+        "ms_per_step": round(us / 1e3, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f16", "data": "synthetic",
+        "config": {"workload": "decoder layer projections at hidden 2048 (Q,K,V,O 2048x2048, gate/up 2048x5632, "
+                               f"down 5632x2048), N={N}, through the layer driver: Q|K|V one launch, O, gate|up one "
+                               "launch + SwiGLU to fp16 h, down(h), one graph over consecutive layers",
+                   "n": N, "layouts": layers[0].layouts, "layers_in_graph": copies,
+                   "timing": "HIP graph replay, HIP events on the launch stream",
+                   "weights": "int4 superblocks (144 B per 256 weights)", "activations": "fp16", "output": "fp32"},
+        "per_launch": per_part,
+        "roofline": {"bound": "hbm", "achieved": round(bytes_layer / us / 1e3, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(bytes_layer / us / 1e3 / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": f"layer: {bytes_layer} algorithmic B per layer / {us:.2f} us per layer"},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
 def run_layer(args) -> int:
     """One decoder layer's projections (Q, K, V, O, gate, up, down) at N = 16,
     back to back on one stream, each on its own weights; the layer's weights
     rotate over enough copies (>= 300 MB) that no projection is served from
     the Infinity Cache.  A step is one layer."""
     import torch
+    if args.driver:
+        return run_layer_driver(args)
     from moat_amd import _lib
     from moat_amd.dequant import _gemm_into, _multi_into, _swiglu_into, quantize_to_superblocks
 

@@ -294,6 +294,19 @@ int32_t moat_int4_gemm_swiglu(const uint16_t* x_f16, const uint8_t* gate_superbl
                               void* workspace, int64_t workspace_bytes, hipStream_t stream);
 
 /*
+ * The SwiGLU step alone, for a GEMM that produced gate and up side by side
+ * (gu[r][0..m) = g, gu[r][m..2m) = u, rows ld floats apart): h[r][c] =
+ * fp16(silu(g) * u) with moat_int4_gemm_swiglu's arithmetic (fp32 g and u,
+ * silu(g) = g / (1 + exp(-g)), one rounding to fp16).  The activation of
+ * antigravity-engine/src/transformer_engine.mm:694-713 /
+ * antigravity-engine/src/shaders/transformer_ops.metal:216-232 after a
+ * strip-order GEMM over [W_gate | W_up].  m % 4 == 0, ld >= 2m, ld % 4 == 0;
+ * gu 16-byte aligned, h 8-byte aligned.
+ */
+int32_t moat_int4_swiglu_f32(const float* gu_f32, int32_t n, int32_t m, int64_t ld, uint16_t* h_f16,
+                             hipStream_t stream);
+
+/*
  * Group quantizer: for each group of group_size values (w_dtype F32, F16 or F64;
  * F64 is rounded to float32 first, as astype(np.float32) does),
  * alpha = max|w|, s = (alpha == 0 ? 1 : alpha / 7) in float32; q =

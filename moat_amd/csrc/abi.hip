@@ -49,6 +49,7 @@ hipError_t launch_gemm(int algo, const uint16_t* x, const uint8_t* sb, float* y,
                        int batch, int finish, int front, int group, int waves, float* partials,
                        uint32_t* counters, uint32_t* status, int tile_order, hipStream_t stream);
 hipError_t launch_records_to_tiles(const uint8_t* sb, int k, int m, uint8_t* tiles, hipStream_t stream);
+hipError_t launch_swiglu_f32(const float* gu, int n, int m, int64_t ld, uint16_t* h, hipStream_t stream);
 hipError_t launch_stream_read(const void* src, int64_t bytes, uint32_t* sink, int blocks, hipStream_t st);
 hipError_t launch_gemm_strips(const uint16_t* x, const uint8_t* w, float* y, int n, int k, int m, int wgs, int depth,
                               int waves, float* slots, uint32_t* status, hipStream_t stream);
@@ -752,6 +753,14 @@ int32_t moat_int4_to_f16(const void* src, int32_t src_dtype, int64_t n, uint16_t
   if (!src || !out_f16) return MOAT_ERR_INVALID;
   if (!aligned(src, src_dtype == MOAT_DTYPE_F64 ? 8 : 4) || !aligned(out_f16, 2)) return MOAT_ERR_INVALID;
   return status_of(moat::launch_to_f16(src, src_dtype, n, out_f16, stream));
+}
+
+int32_t moat_int4_swiglu_f32(const float* gu_f32, int32_t n, int32_t m, int64_t ld, uint16_t* h_f16,
+                             hipStream_t stream) {
+  if (n < 0 || m < 0 || (m % 4) != 0 || ld < 2 * (int64_t)m || (ld % 4) != 0) return MOAT_ERR_INVALID;
+  if (n == 0 || m == 0) return MOAT_OK;
+  if (!gu_f32 || !h_f16 || !aligned(gu_f32, 16) || !aligned(h_f16, 8)) return MOAT_ERR_INVALID;
+  return status_of(moat::launch_swiglu_f32(gu_f32, n, m, ld, h_f16, stream));
 }
 
 int32_t moat_int4_i8_div_to_f16(const int8_t* q, int64_t n, float divisor, uint16_t* out_f16, hipStream_t stream) {

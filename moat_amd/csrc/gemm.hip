@@ -146,6 +146,31 @@ __device__ __forceinline__ uint2 swiglu4(float4_t g, float4_t u) {
   return uint2{o[0], o[1]};
 }
 
+// h[r][c] = fp16(silu(g) * u), g = gu[r][c], u = gu[r][m + c] (rows ld floats
+// apart): the SwiGLU step on the output of one GEMM over gate and up stored
+// side by side, with swiglu4's arithmetic.  Four columns a thread.
+__global__ void __launch_bounds__(256) swiglu_f32_kernel(const float* __restrict__ gu, int n, int m, int64_t ld,
+                                                         uint16_t* __restrict__ h) {
+  const int64_t quads = (int64_t)n * (m / 4);
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < quads; e += stride) {
+    const int64_t r = e / (m / 4);
+    const int c = (int)(e - r * (m / 4)) * 4;
+    const float4_t g = *reinterpret_cast<const float4_t*>(gu + r * ld + c);
+    const float4_t u = *reinterpret_cast<const float4_t*>(gu + r * ld + m + c);
+    *reinterpret_cast<uint2*>(h + r * m + c) = swiglu4(g, u);
+  }
+}
+
+hipError_t launch_swiglu_f32(const float* gu, int n, int m, int64_t ld, uint16_t* h, hipStream_t stream) {
+  const int64_t quads = (int64_t)n * (m / 4);
+  if (quads == 0) return hipSuccess;
+  int64_t blocks = (quads + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  hipLaunchKernelGGL(swiglu_f32_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, gu, n, m, ld, h);
+  return hipGetLastError();
+}
+
 // Round range of split s (no device-side division).
 __device__ __forceinline__ void split_rounds(const GemmParams& P, int split, int& r_begin, int& r_end) {
   r_begin = split * P.rounds_base + min(split, P.rounds_rem);

@@ -165,6 +165,14 @@ def test_fused_entry_points_validate(lib):
     assert lib.moat_int4_gemm_multi(ctypes.c_void_p(0x10008), sbs, ys, 2, 1, 2048, 2048, None, 0, None) == I  # x 16 B
     assert lib.moat_int4_gemm_swiglu(FAKE, FAKE, FAKE, ctypes.c_void_p(0x10004), 1, 2048, 2048, None, 0, None) == I
     assert lib.moat_int4_gemm_swiglu(FAKE, None, FAKE, FAKE, 1, 2048, 2048, None, 0, None) == I
+    # the SwiGLU step alone: m % 4, ld >= 2m and ld % 4, 16 B gate/up rows, 8 B h
+    assert lib.moat_int4_swiglu_f32(FAKE, 1, 6, 12, FAKE, None) == I
+    assert lib.moat_int4_swiglu_f32(FAKE, 1, 8, 12, FAKE, None) == I
+    assert lib.moat_int4_swiglu_f32(FAKE, 1, 8, 18, FAKE, None) == I
+    assert lib.moat_int4_swiglu_f32(ctypes.c_void_p(0x10008), 1, 8, 16, FAKE, None) == I
+    assert lib.moat_int4_swiglu_f32(FAKE, 1, 8, 16, ctypes.c_void_p(0x10004), None) == I
+    assert lib.moat_int4_swiglu_f32(FAKE, -1, 8, 16, FAKE, None) == I
+    assert lib.moat_int4_swiglu_f32(None, 0, 8, 16, None, None) == _lib.MOAT_OK
     # a shared-tile plan needs the workspace: refused before any launch
     size = lib.moat_int4_gemm_swiglu_workspace_size(16, 2048, 5632)
     if size > 0:
