@@ -38,6 +38,7 @@ CONFIGS = {
     "k3072_m8192": (3072, 8192, 0.02, 1003, 0.0, [1, 2, 4, 8, 16, 32]),
     "k8192_m28672": (8192, 28672, 0.01, 1005, 0.001, [1, 32]),
     "k2048_m32000": (2048, 32000, 0.02, 1006, 0.0, [1, 2, 4, 8, 16, 32]),
+    "k4096_m14336": (4096, 14336, 0.02, 1007, 0.0, [1, 2, 4, 8, 16, 32]),
 }
 WORKLOAD_NAMES = {
     "k2048_m2048": "int4 superblock projection 2048x2048",
@@ -45,6 +46,7 @@ WORKLOAD_NAMES = {
     "k3072_m8192": "int4 superblock FFN projection K=3072 M=8192, N sweep 1..32",
     "k8192_m28672": "int4 superblock projection K=8192 M=28672 (70B-class FFN, 0.1% 8-sigma outliers)",
     "k2048_m32000": "int4 superblock LM head K=2048 (hidden) x M=32000 (vocabulary), N sweep 1..32",
+    "k4096_m14336": "int4 superblock FFN projection K=4096 M=14336 (8B-class), N sweep 1..32",
 }
 ROTATE_BYTES = 300 * 1024 * 1024
 DEFAULT_CONFIG = "k3072_m8192"
@@ -275,7 +277,8 @@ def measure_projection(torch, timer, lib, config, ns, layout, args, with_floor=T
 
     def call(N, i):
         _gemm_into(xs[N], blobs[i % copies], ys[N], K, M, args.algo, args.splits, args.batch, args.finish,
-                   args.front, waves=args.waves, tile_order=layout == "tile", strip_order=layout == "strip")
+                   args.front, group=args.group, waves=args.waves, tile_order=layout == "tile",
+                   strip_order=layout == "strip")
 
     with torch.cuda.stream(timer.cap):
         for N in ns:  # creates this stream's workspace before any capture
@@ -340,6 +343,9 @@ def main() -> int:
     ap.add_argument("--batch", type=int, default=0, help="rounds of loads issued together (0 auto)")
     ap.add_argument("--finish", type=int, default=0, help="split-K hand-off (0 auto, 1 atomics, 2 fences, 3 kernel)")
     ap.add_argument("--waves", type=int, default=0, help="waves per workgroup, 4 or 8 (0 auto)")
+    ap.add_argument("--group", type=int, default=0,
+                    help="row order: tile groups (0 auto); strip order: 0 auto, 1 the strip-group kernel (N > 8), "
+                         "2 the strip kernel 8 rows a launch, 3 the wide strip kernel")
     ap.add_argument("--front", type=int, default=0,
                     help="load front end (0 auto, 1 LDS-staged, 2 direct, 3 LDS DMA, 4 record stream)")
     ap.add_argument("--tile-order", action="store_true",

@@ -210,12 +210,15 @@ int32_t moat_int4_gemm_tiles(const uint16_t* x_f16, const uint8_t* tiles, float*
  * moat_int4_gemm_strips: Y = X @ deq(W) over a strip-order stream, the same
  * product and tolerance as moat_int4_gemm.  Preconditions: 1 <= n <= 32,
  * k >= 2048, k % 32 == 0, m % 32 == 0; x 16-byte aligned, strips 16-byte
- * aligned, y 4-byte aligned (MOAT_ERR_INVALID otherwise).  Rows of X are
- * taken 8 per launch.  Workspace as for moat_int4_gemm (zeroed once, left
- * zero, shares the status word), sized by
- * moat_int4_gemm_strips_workspace_size; options: `splits` = workgroups
- * (0 automatic), `batch` = ring depth (2..4, 0 automatic), `waves` = waves
- * per workgroup (4, 8 or 12; 0 automatic), the rest ignored.
+ * aligned, y 4-byte aligned (MOAT_ERR_INVALID otherwise).  All N rows run in
+ * one launch.  Workspace as for moat_int4_gemm (zeroed once, left zero,
+ * shares the status word), sized by moat_int4_gemm_strips_workspace_size;
+ * options: `splits` = workgroups (0 automatic), `group` = kernel (0
+ * automatic; 1 the strip-group kernel for N > 8; 2 the strip kernel, 8 rows
+ * a launch; 3 the wide strip kernel), `batch` = ring depth of the strip
+ * kernel (2..4) or the strip-group kernel (2 or 3), 0 automatic, `waves` =
+ * waves per workgroup of the strip kernel (4, 8 or 12; 0 automatic), the
+ * rest ignored.
  */
 int32_t moat_int4_records_to_strips(const uint8_t* superblocks, int32_t k, int32_t m, uint8_t* strips,
                                     hipStream_t stream);

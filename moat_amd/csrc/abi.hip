@@ -57,6 +57,8 @@ hipError_t launch_records_to_strips(const uint8_t* sb, int k, int m, uint8_t* st
 hipError_t launch_strips_to_records(const uint8_t* strips, int k, int m, uint8_t* sb, hipStream_t stream);
 int strips_waves(int n, int waves);
 int strips_depth(int n, int waves, int depth);
+hipError_t launch_gemm_strips_wide(const uint16_t* x, const uint8_t* w, float* y, int n, int k, int m, int wgs,
+                                   float* slots, uint32_t* status, hipStream_t stream);
 hipError_t launch_gemm_strip_groups(const uint16_t* x, const uint8_t* w, float* y, int n, int k, int m, int wgs,
                                     int depth, float* slots, uint32_t* status, hipStream_t stream);
 int strip_groups_slot_bytes(int n);
@@ -416,39 +418,57 @@ constexpr int64_t kStripMaxWorkgroups = 256;
 bool strips_shape_ok(int32_t n, int32_t k, int32_t m) {
   if (n < 1 || n > kMaxN || k < 2048 || (k % 32) != 0 || m < 32 || (m % 32) != 0) return false;
   if ((int64_t)(m / 32) * (k / 32) > ((int64_t)1 << 30)) return false;  // unit indices are 32-bit
-  if ((int64_t)kStripRowsPerLaunch * k * 2 > ((int64_t)1 << 31)) return false;  // X offsets are 32-bit
+  if ((int64_t)kMaxN * k * 2 > ((int64_t)1 << 31)) return false;  // X offsets are 32-bit
   return true;
 }
 
 struct StripPlan {
-  bool groups;  // N > 8 in one launch of the strip-group kernel
+  int kind;  // kStripSlices, kStripGroups or kStripWide
   int wgs;
   int depth;
   int waves;
   int64_t workspace_bytes;
 };
 
+// Kernel choice (options `group`): 0 automatic, 1 the strip-group kernel
+// (N > 8), 2 the strip kernel (8 rows a launch), 3 the wide strip kernel.
+constexpr int kStripSlices = 0, kStripGroups = 1, kStripWide = 2;
+
 bool strip_options_ok(const moat_int4_gemm_options* o) {
-  return !o || (o->splits >= 0 && o->batch >= 0 && (o->waves == 0 || o->waves == 4 || o->waves == 8 || o->waves == 12));
+  return !o || (o->splits >= 0 && o->batch >= 0 && (o->waves == 0 || o->waves == 4 || o->waves == 8 || o->waves == 12) &&
+                o->group >= 0 && o->group <= 3);
 }
 
-// N <= 8: the strip kernel.  Workgroups: one whole strip each when M/32 is
+// The strip kernel: workgroups, one whole strip each when M/32 is
 // 128..256 (nothing shared); otherwise up to 256 (one per CU: the kernel's
 // LDS leaves room for one), at least 16 units each.  Shared strips need the
 // status word and one slot of 8 x 32 floats per workgroup, after the fixed
 // 64 KB block.
-// N > 8: the strip-group kernel over (group of 8 strips, unit) items when the
-// records span fewer than 2^32 bytes (its copy offsets are 32-bit; larger
-// matrices run the strip kernel 8 rows at a time): up to 256 workgroups of
-// at least 16 items, and slots of 8 waves x 2 or 4 KB per workgroup.
+// The wide strip kernel: all N rows in one launch, the same workgroup ranges
+// and hand-off, slots of N x 32 floats per workgroup.  The strip-group
+// kernel, over (group of 8 strips, unit) items when the records span fewer
+// than 2^32 bytes (its copy offsets are 32-bit): up to 256 workgroups of at
+// least 16 items and slots of 8 waves x 2 or 4 KB per workgroup.
 StripPlan plan_strips(int32_t n, int32_t k, int32_t m, const moat_int4_gemm_options* o) {
   StripPlan p;
   const int64_t strips = m / 32, units = k / 32;
-  // (two 8-row launches of the strip kernel measured faster than one
-  // strip-group launch for 9..16 rows of matrices under 2^26 weights)
-  const bool small16 = n <= 16 && (int64_t)k * m < ((int64_t)1 << 26);
-  p.groups = n > kStripRowsPerLaunch && !small16 && strips * units * 576 < ((int64_t)1 << 32);
-  if (p.groups) {
+  const int forced = o ? o->group : 0;
+  const bool groups_fit = strips * units * 576 < ((int64_t)1 << 32);
+  const int64_t weights = (int64_t)k * m;
+  p.kind = kStripSlices;
+  if (forced == 3) {
+    p.kind = kStripWide;
+  } else if (forced == 1) {
+    if (n > kStripRowsPerLaunch && groups_fit) p.kind = kStripGroups;
+  } else if (forced == 0) {
+    // measured: the wide kernel is the fastest for N >= 5 and, on matrices
+    // under 2^25 weights, for every N; the strip kernel (1, 2 or 4 rows
+    // staged, longer stages) for N <= 4 on larger ones; the strip-group
+    // kernel (X staged once for 8 strips) for N > 16 from 2^27 weights
+    if (n > 16 && weights >= ((int64_t)1 << 27) && groups_fit) p.kind = kStripGroups;
+    else if (n >= 5 || weights < ((int64_t)1 << 25)) p.kind = kStripWide;
+  }
+  if (p.kind == kStripGroups) {
     const int64_t total = (strips + 7) / 8 * units;
     int64_t wgs;
     if (o && o->splits > 0) wgs = o->splits < kStripMaxWorkgroups ? o->splits : kStripMaxWorkgroups;
@@ -469,13 +489,19 @@ StripPlan plan_strips(int32_t n, int32_t k, int32_t m, const moat_int4_gemm_opti
   else wgs = total / 16 < 256 ? (total / 16 > 0 ? total / 16 : 1) : 256;
   if (wgs > total) wgs = total;
   p.wgs = (int)wgs;
+  const int64_t base = total / wgs, rem = total % wgs;
+  const bool shared = !(rem == 0 && base % units == 0);
+  if (p.kind == kStripWide) {  // 8 waves, a two-stage ring; slots of n x 32 floats
+    p.waves = 8;
+    p.depth = 2;
+    p.workspace_bytes = shared ? kCounterBlockBytes + wgs * n * 32 * (int64_t)sizeof(float) : 0;
+    return p;
+  }
   const int rows = n < kStripRowsPerLaunch ? n : kStripRowsPerLaunch;
   // 12 waves (4-unit stages) for ranges of at most 256 units, 8 beyond
   const int waves = o && o->waves ? o->waves : (total / wgs <= 256 ? 12 : 8);
   p.waves = moat::strips_waves(rows, waves);
   p.depth = moat::strips_depth(rows, p.waves, o ? o->batch : 0);
-  const int64_t base = total / wgs, rem = total % wgs;
-  const bool shared = !(rem == 0 && base % units == 0);
   p.workspace_bytes = shared ? kCounterBlockBytes + wgs * kStripRowsPerLaunch * 32 * (int64_t)sizeof(float) : 0;
   return p;
 }
@@ -573,9 +599,11 @@ int32_t moat_int4_gemm_strips(const uint16_t* x_f16, const uint8_t* strips, floa
     status = static_cast<uint32_t*>(workspace);
     slots = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + kCounterBlockBytes);
   }
-  if (p.groups)
+  if (p.kind == kStripGroups)
     return status_of(moat::launch_gemm_strip_groups(x_f16, strips, y_f32, n, k, m, p.wgs, p.depth, slots, status,
                                                     stream));
+  if (p.kind == kStripWide)
+    return status_of(moat::launch_gemm_strips_wide(x_f16, strips, y_f32, n, k, m, p.wgs, slots, status, stream));
   // 8 rows of X per launch; the launches share the workspace in stream order
   for (int32_t r0 = 0; r0 < n; r0 += kStripRowsPerLaunch) {
     const int32_t rows = n - r0 < kStripRowsPerLaunch ? n - r0 : kStripRowsPerLaunch;

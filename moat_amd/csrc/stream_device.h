@@ -94,8 +94,12 @@ __device__ __forceinline__ void status_to_lds(const uint32_t* status, uint32_t* 
 // copy.
 constexpr int kStatusLdsBytes = 256;
 
+// (An LDS read, ds_read_b32: through a generic pointer the volatile read
+// would be a flat load, which also waits for vmcnt, i.e. for every copy in
+// flight.)
+typedef __attribute__((address_space(3))) const volatile uint32_t lds_cv_u32;
 __device__ __forceinline__ uint32_t status_from_lds(const uint32_t* lds_word) {
-  return *reinterpret_cast<const volatile uint32_t*>(lds_word);
+  return *(lds_cv_u32*)lds_word;
 }
 
 // A value to add to every result: 0 when the status word read at the start

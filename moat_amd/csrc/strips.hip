@@ -156,16 +156,17 @@ __device__ __forceinline__ float4_t load16_coherent(const float* base, uint32_t 
 // workgroups p+1 .. p+kStripPrefetch).
 constexpr int kStripPrefetch = 2;
 
-// Output of one part of a strip by one wave (the part's sums of the W
-// waves are in `sl`, wave-major): lanes l < n * 8 each hold four columns of
-// one row.  `pre` holds the contributions of the first `npre` later
-// workgroups when the caller loaded them ahead (npre = 0: none).
+// Output of rows row0 .. row0+7 of one part of a strip by one wave (the
+// part's sums of the W waves are in `sl`, wave-major, NX rows each): lane l
+// holds four columns of row row0 + l / 8 (rows past N idle).  `pre` holds
+// the contributions of the first `npre` later workgroups when the caller
+// loaded them ahead (npre = 0: none).
 template <int NX, int W>
 __device__ __forceinline__ void strip_part_out(const StripParams& P, const float* sl, int p, int strip, bool whole,
                                                bool owner, int last_unit, float poison,
-                                               const float4_t (&pre)[kStripPrefetch], int npre) {
+                                               const float4_t (&pre)[kStripPrefetch], int npre, int row0 = 0) {
   const int lane = threadIdx.x & 63;
-  const int r = lane >> 3, c4 = 4 * (lane & 7);
+  const int r = row0 + (lane >> 3), c4 = 4 * (lane & 7);
   const bool active = r < P.n;
   float4_t v = {0.f, 0.f, 0.f, 0.f};
   if (active) {
@@ -569,6 +570,270 @@ hipError_t launch_gemm_strips(const uint16_t* x, const uint8_t* w, float* y, int
 }
 
 // ---------------------------------------------------------------------------
+// Wide strips: the strip kernel's walk for 9 <= N <= 32 in one launch.
+//  * the same unit ranges, stages, ring and hand-off as the strip kernel,
+//    with 8 waves and 16 or 32 rows of X (one or two 16-row MFMA tiles on
+//    the same decoded weights), so that a strip's weights are read once for
+//    all N rows and, where the plan gives each workgroup whole strips,
+//    nothing is handed between workgroups;
+//  * a wave's stage holds 4 (16 rows) or 2 (32 rows) units: its X is 4 KB,
+//    rows kRowChunks 16-byte chunks apart, copied as 4 copies of 1 KB that
+//    each cover 4 or 8 whole rows; chunk c of row r sits at position
+//    c ^ wide_swz(r) of its row, so that one quarter of 16 rows falls on 16
+//    different 16-byte bank groups;
+//  * at a strip boundary every wave leaves its sums in LDS, and 2 or 4 waves
+//    each reduce and write (or hand off) 8 rows of the part.
+constexpr int kWideWaves = 8;
+
+template <int NT>
+struct WideGeom {
+  static constexpr int kRows = 16 * NT;                          // X rows staged (rows past N repeat row N - 1)
+  static constexpr int kStageUnits = NT == 1 ? 4 : 2;            // a wave's units a stage
+  static constexpr int kWChunks = 36 * kStageUnits;              // 144, 72
+  static constexpr int kWLoads = (kWChunks + 63) / 64;           // 3, 2
+  static constexpr int kWTail = kWChunks - 64 * (kWLoads - 1);   // lanes of the last weight copy: 16, 8
+  static constexpr int kWStage = 16 * kWChunks;                  // 2304, 1152
+  static constexpr int kRowChunks = 4 * kStageUnits;             // 16-byte chunks of a row's stage: 16, 8
+  static constexpr int kXStage = kRows * 16 * kRowChunks;        // 4096
+  static constexpr int kXLoads = kXStage / 1024;                 // 4
+  static constexpr int kLS = kWLoads + kXLoads;                  // copies a stage
+  static constexpr int kSlotBytes = kRows * kStripCols * 4;      // one wave's sums of a part
+  static constexpr int kPasses = kRows / 8;                      // output waves of a part
+  template <int kDepth>
+  static constexpr int wave_bytes() { return kDepth * (kWStage + kXStage); }
+  template <int kDepth>
+  static constexpr size_t lds_bytes() {
+    return (size_t)kWideWaves * wave_bytes<kDepth>() + (size_t)2 * kWideWaves * kSlotBytes + kStatusLdsBytes;
+  }
+};
+
+template <int NT>
+__device__ __forceinline__ int wide_swz(int r) { return NT == 1 ? (r & 15) : ((r >> 1) & 7); }
+
+template <int NT, int kDepth>
+__global__ void __launch_bounds__(kWideWaves * 64) int4_gemm_strips_wide_kernel(StripParams P) {
+  using G = WideGeom<NT>;
+  constexpr int W = kWideWaves;
+  constexpr int kSU = G::kStageUnits;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int q = lane >> 4, j = lane & 15;
+  const int p = blockIdx.x;
+  const int U = P.units;
+  const int lo = p * P.base + min(p, P.rem);
+  const int hi = lo + P.base + (p < P.rem ? 1 : 0);
+  const MagicWords mw = magic_words();
+
+  // Weight copies: slot s = 64 i + lane of a stage carries chunk s % 36 of
+  // the stage's unit s / 36 (the stage's units lie W units apart); units
+  // past the range re-load the stage's first unit.
+  uint32_t woff[G::kWLoads], wfirst[G::kWLoads];
+  int wunit[G::kWLoads];
+#pragma unroll
+  for (int i = 0; i < G::kWLoads; ++i) {
+    const int s = min(64 * i + lane, G::kWChunks - 1);  // lanes past the last chunk copy nothing
+    wunit[i] = s / 36;
+    wfirst[i] = (uint32_t)(16 * (s % 36));
+    woff[i] = (uint32_t)(W * kUnitBytes * wunit[i]) + wfirst[i];
+  }
+  // X copies: copy i, lane l fills position 64 i + l of the stage: row
+  // r = position / kRowChunks, chunk c = (position % kRowChunks) ^
+  // wide_swz(r), i.e. quarter c % 4 of the stage's unit c / 4 (rows past N
+  // read row N - 1)
+  uint32_t xoff[G::kXLoads];
+  int xk[G::kXLoads];
+#pragma unroll
+  for (int i = 0; i < G::kXLoads; ++i) {
+    const int pos = 64 * i + lane;
+    const int r = pos / G::kRowChunks;
+    const int c = (pos % G::kRowChunks) ^ wide_swz<NT>(r);
+    xk[i] = c >> 2;
+    xoff[i] = (uint32_t)(2 * (min(r, P.n - 1) * P.k + 8 * (c & 3)));
+  }
+  // LDS reads of unit k of a stage: record q's 8 row scales, the 8 bytes of
+  // column pair j, and quarter q of X row 16 tt + j
+  const uint32_t rsc = 144 * q, rpay = 144 * q + 16 + 8 * j;
+  uint32_t rx[NT][kSU];
+#pragma unroll
+  for (int tt = 0; tt < NT; ++tt) {
+    const int r = 16 * tt + j;
+#pragma unroll
+    for (int k = 0; k < kSU; ++k) rx[tt][k] = (uint32_t)(16 * (G::kRowChunks * r + ((4 * k + q) ^ wide_swz<NT>(r))));
+  }
+
+  uint8_t* wring = smem + wave * G::template wave_bytes<kDepth>();
+  uint8_t* xring = wring + kDepth * G::kWStage;
+  const uint32_t wring_lds = (uint32_t)(uintptr_t)(lds_ptr_t)wring;
+  const uint32_t xring_lds = (uint32_t)(uintptr_t)(lds_ptr_t)xring;
+  float* slots = reinterpret_cast<float*>(smem + W * G::template wave_bytes<kDepth>());
+  uint32_t* lds_status =
+      reinterpret_cast<uint32_t*>(smem + W * G::template wave_bytes<kDepth>() + 2 * W * G::kSlotBytes);
+  status_to_lds(P.status, lds_status);  // the wave's oldest copy: the first ring wait covers it
+
+  const int first = lo + wave;  // this wave's units: first + W i
+  const int cnt = first < hi ? (hi - first + W - 1) / W : 0;
+  const int nst = (cnt + kSU - 1) / kSU;
+  int ub_issue = first % U;  // strip-relative unit of the next stage's first unit
+
+  auto issue = [&](int s) {
+    const int u0 = first + W * kSU * s;
+    const uint8_t* base = P.w + (uint64_t)u0 * kUnitBytes;
+    const uint32_t wst = __builtin_amdgcn_readfirstlane(wring_lds + (s % kDepth) * G::kWStage);
+#pragma unroll
+    for (int i = 0; i < G::kWLoads; ++i) {
+      const uint32_t off = u0 + W * wunit[i] < hi ? woff[i] : wfirst[i];
+      if (i < G::kWLoads - 1 || lane < G::kWTail) lds_dma16(base, off, wst + 1024 * i);
+    }
+    const uint32_t xst = __builtin_amdgcn_readfirstlane(xring_lds + (s % kDepth) * G::kXStage);
+#pragma unroll
+    for (int i = 0; i < G::kXLoads; ++i) {
+      int t = ub_issue + W * xk[i];
+      if (t >= U) t -= U;  // U >= 64 > W * xk
+      lds_dma16(P.x, xoff[i] + 64u * (uint32_t)t, xst + 1024 * i);
+    }
+    ub_issue += W * kSU;
+    while (ub_issue >= U) ub_issue -= U;
+  };
+#pragma unroll
+  for (int s = 0; s < kDepth - 1; ++s)
+    if (s < nst) issue(s);
+  if (nst == 0) wait_vmcnt<0>();  // no ring wait will cover the status copy
+
+  const int strip0 = lo / U;
+  const int nparts = hi > lo ? (hi - 1) / U - strip0 + 1 : 0;
+  int part = 0;
+  int part_end = min(hi, (strip0 + 1) * U);
+
+  float4_t acc[NT][2];
+#pragma unroll
+  for (int tt = 0; tt < NT; ++tt) acc[tt][0] = acc[tt][1] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+  const float4_t no_pre[kStripPrefetch] = {};
+  auto flush = [&](int pi) {
+    float* sl = slots + ((pi & 1) * W + wave) * G::kRows * kStripCols;
+    // tile tt, lane (q, j): rows 16 tt + 4 q + v, columns 2 j and 2 j + 1
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        *reinterpret_cast<float2*>(sl + (16 * tt + 4 * q + v) * kStripCols + 2 * j) = float2{acc[tt][0][v], acc[tt][1][v]};
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt) acc[tt][0] = acc[tt][1] = float4_t{0.f, 0.f, 0.f, 0.f};
+    lds_barrier();
+    // rows 8 rp .. 8 rp + 7 of the part: wave (kPasses pi + rp) % W
+    const int rp = (wave - (G::kPasses * pi) % W + W) % W;
+    if (rp < G::kPasses && 8 * rp < P.n) {
+      const int strip = strip0 + pi;
+      const int a = max(lo, strip * U), b = min(hi, (strip + 1) * U);
+      const bool whole = a == strip * U && b == (strip + 1) * U;
+      const bool owner = !whole && a == strip * U;
+      strip_part_out<G::kRows, W>(P, slots + (pi & 1) * W * G::kRows * kStripCols, p, strip, whole, owner,
+                                  (strip + 1) * U - 1, status_poison(status_from_lds(lds_status)), no_pre, 0,
+                                  8 * rp);
+    }
+  };
+
+  struct UnitRegs {
+    half8_t a[NT];
+    uint4 sc;
+    uint2 b;
+  };
+  auto load_unit = [&](UnitRegs& r, const uint8_t* wst, const uint8_t* xst, int k) {
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt) r.a[tt] = *reinterpret_cast<const half8_t*>(xst + rx[tt][k]);
+    r.sc = *reinterpret_cast<const uint4*>(wst + kUnitBytes * k + rsc);
+    r.b = *reinterpret_cast<const uint2*>(wst + kUnitBytes * k + rpay);
+  };
+  auto math_unit = [&](const UnitRegs& r) {
+    // r.b.x holds rows 0, 2, 1, 3 of column pair j, r.b.y rows 4, 6, 5, 7
+    const uint32_t words[4] = {r.b.x, r.b.x >> 8, r.b.y, r.b.y >> 8};
+    const uint32_t scp[4] = {r.sc.x, r.sc.y, r.sc.z, r.sc.w};
+    half8_t b0, b1;
+#pragma unroll
+    for (int pp = 0; pp < 4; ++pp) {
+      const half2_t s2 = bitcast<half2_t>(scp[pp]);
+      const half2_t lo2 = nib_lo_pair(words[pp], mw.lo) * s2;
+      const half2_t hi2 = nib_hi_pair(words[pp], mw.hi) * s2;
+      b0[2 * pp] = lo2[0];
+      b0[2 * pp + 1] = lo2[1];
+      b1[2 * pp] = hi2[0];
+      b1[2 * pp + 1] = hi2[1];
+    }
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt) {
+      acc[tt][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(r.a[tt], b0, acc[tt][0], 0, 0, 0);
+      acc[tt][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(r.a[tt], b1, acc[tt][1], 0, 0, 0);
+    }
+  };
+
+  for (int s = 0; s < nst; ++s) {
+    if (s + kDepth - 1 < nst) issue(s + kDepth - 1);
+    const int ahead = min(kDepth - 1, nst - 1 - s);  // stages issued after this one
+    if (ahead >= 3) wait_vmcnt<3 * G::kLS>();
+    else if (ahead == 2) wait_vmcnt<2 * G::kLS>();
+    else if (ahead == 1) wait_vmcnt<G::kLS>();
+    else wait_vmcnt<0>();
+    const uint8_t* wst = wring + (s % kDepth) * G::kWStage;
+    const uint8_t* xst = xring + (s % kDepth) * G::kXStage;
+    const int kmax = min(kSU, cnt - kSU * s);
+    static_assert(W * (kSU - 1) < 64, "a stage spans fewer units than a strip");
+    int kb = part_end - (first + W * kSU * s);
+    kb = kb <= 0 ? 0 : min(kmax, (kb + W - 1) / W);
+    // units [k_begin, k_end) of the stage, every read of the stage issued
+    // before its arithmetic where the whole stage is in range
+    auto run_units = [&](int k_begin, int k_end) {
+      if (k_begin == 0 && k_end == kSU) {
+        UnitRegs r[kSU];
+#pragma unroll
+        for (int k = 0; k < kSU; ++k) load_unit(r[k], wst, xst, k);
+#pragma unroll
+        for (int k = 0; k < kSU; ++k) math_unit(r[k]);
+      } else {
+#pragma unroll
+        for (int k = 0; k < kSU; ++k)
+          if (k >= k_begin && k < k_end) {
+            UnitRegs r;
+            load_unit(r, wst, xst, k);
+            math_unit(r);
+          }
+      }
+    };
+    run_units(0, kb);
+    if (kb < kmax) {
+      flush(part);
+      ++part;
+      part_end = min(hi, part_end + U);
+      run_units(kb, kmax);
+    }
+  }
+  for (; part < nparts; ++part) flush(part);
+}
+
+constexpr size_t kWideMaxLds = 156 * 1024;
+
+template <int NT>
+static hipError_t launch_wide_one(const StripParams& P, int wgs, hipStream_t stream) {
+  const size_t lds = WideGeom<NT>::template lds_bytes<2>();
+  static_assert(WideGeom<NT>::template lds_bytes<2>() <= kWideMaxLds, "a two-stage ring must fit");
+  hipLaunchKernelGGL((int4_gemm_strips_wide_kernel<NT, 2>), dim3(wgs), dim3(kWideWaves * 64), lds, stream, P);
+  return hipGetLastError();
+}
+
+hipError_t launch_gemm_strips_wide(const uint16_t* x, const uint8_t* w, float* y, int n, int k, int m, int wgs,
+                                   float* slots, uint32_t* status, hipStream_t stream) {
+  StripParams P = {};
+  P.x = x; P.w = w; P.y = y; P.slots = slots; P.status = status;
+  P.n = n; P.k = k; P.m = m;
+  P.units = k / kUnitRows;
+  const int total = (m / kStripCols) * P.units;
+  P.base = total / wgs;
+  P.rem = total % wgs;
+  P.y_vec = (reinterpret_cast<uintptr_t>(y) & 15) == 0 ? 1 : 0;
+  return n <= 16 ? launch_wide_one<1>(P, wgs, stream) : launch_wide_one<2>(P, wgs, stream);
+}
+
+// ---------------------------------------------------------------------------
 // Strip groups: the GEMM over strip order for 9 <= N <= 32 in one pass.
 //  * strips are taken 8 at a time (a group, 256 columns); the (group, unit)
 //    items form one stream (group-major), and workgroup p takes an equal
@@ -612,6 +877,11 @@ struct GroupParams {
   int strips;          // m / 32
   int base, rem;       // workgroup p covers items [p*base + min(p, rem), +base + (p < rem))
   int y_vec8;          // y 8-byte aligned
+};
+
+template <bool B>
+struct FlushTag {
+  static constexpr bool value = B;
 };
 
 template <int NT>
@@ -720,9 +990,14 @@ __global__ void __launch_bounds__(kGroupWaves * 64) int4_gemm_strip_groups_kerne
 
   // Group boundary.  Every wave of the workgroup flushes the same part at
   // the same point (they walk the same units), so the hand-off can use
-  // workgroup barriers: one flag and one release per contributing workgroup.
+  // workgroup barriers: one flag per contributing workgroup.  A part that
+  // ends inside the range ends at its group's end, so only the range's last
+  // part can be an owner's: the flushes inside the stage loop store or write
+  // (kLast false: no hand-off loads there, none of their registers pending
+  // across the loop), the one after it may also gather.
   uint32_t* lds_flag = lds_status + 1;  // owner: the poll's outcome, for all waves
-  auto flush = [&]() {
+  auto flush = [&](auto last_tag) {
+    constexpr bool kLast = decltype(last_tag)::value;
     const int strip = kGroupWaves * gcur + wave;
     const int a = max(lo, gcur * U), b = min(hi, (gcur + 1) * U);
     const bool whole = a == gcur * U && b == (gcur + 1) * U;
@@ -738,49 +1013,68 @@ __global__ void __launch_bounds__(kGroupWaves * 64) int4_gemm_strip_groups_kerne
 #pragma unroll
           for (int h = 0; h < 2; ++h) store16_coherent(mine + (2 * tt + h) * 64 + lane, acc[tt][h]);
       }
-      wait_vmcnt<0>();  // this wave's stores have left it
+      // the sums are device-coherent stores: complete (vmcnt counts stores)
+      // in every wave before wave 0 raises the flag
+      wait_vmcnt<0>();
       lds_barrier();
-      if (wave == 0)  // release: every wave's sums reach the device before the flag
-        __hip_atomic_store(flags + p, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+      if (wave == 0) __hip_atomic_store(flags + p, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     } else {
       bool gave_up = false;
-      if (owner) {  // add the later workgroups' sums of this group, in workgroup order
-        const int q_last = group_owner(P, (gcur + 1) * U - 1);
-        if (wave == 0) {  // every later workgroup's flag, then one acquire for all their sums
-          int polls = kMaxPolls;
-          bool all = true;
-          for (int c = p + 1; c <= q_last; ++c) {
-            bool seen;
-            for (;;) {
-              seen = __hip_atomic_load(flags + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
-              if (handoff_stop(seen, polls)) break;
-              --polls;
-              __builtin_amdgcn_s_sleep(1);
+      if constexpr (kLast) {
+        if (owner) {  // add the later workgroups' sums of this group, in workgroup order
+          const int q_last = group_owner(P, (gcur + 1) * U - 1);
+          if (wave == 0) {  // every later workgroup's flag, one lane each, polled together
+            int polls = kMaxPolls;
+            bool all = true;
+            for (int c0 = p + 1; c0 <= q_last; c0 += 64) {
+              const int c = c0 + lane;
+              bool seen = c > q_last;
+              for (;;) {
+                if (!seen) seen = __hip_atomic_load(flags + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
+                if (handoff_stop(__ballot(!seen) == 0ull, polls)) break;
+                --polls;
+                __builtin_amdgcn_s_sleep(1);
+              }
+              all = all && __ballot(!seen) == 0ull;
+              if (c <= q_last) __hip_atomic_store(flags + c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
-            all = all && seen;
-            __hip_atomic_store(flags + c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (!all && lane == 0)
+              __hip_atomic_fetch_or(P.status, kWsStatusHandoffTimeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (lane == 0) *lds_flag = all ? 1u : 0u;
           }
-          if (!all)
-            __hip_atomic_fetch_or(P.status, kWsStatusHandoffTimeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");  // drop cached copies of their slots
-          if (lane == 0) *lds_flag = all ? 1u : 0u;
-        }
-        lds_barrier();
-        gave_up = *reinterpret_cast<volatile uint32_t*>(lds_flag) == 0u;
-        if (strip < P.strips) {
-          for (int c = p + 1; c <= q_last; ++c) {
-            float4_t* theirs = slots4 + (size_t)(c * kGroupWaves + wave) * kChunks;
+          lds_barrier();
+          gave_up = status_from_lds(lds_flag) == 0u;
+          if (strip < P.strips) {
+            // device-coherent loads of kBatch workgroups' sums at a time, all
+            // issued before the first add (past the last workgroup a batch
+            // re-reads the last one's slot), added in workgroup order; then
+            // the slots are cleared (the last one's again, past the end):
+            // the workspace is left as found (zero), since the other kernels
+            // sharing it take any non-zero slot word for a written partial
+            constexpr int kBatch = 8 / NT;
+            for (int c0 = p + 1; c0 <= q_last; c0 += kBatch) {
+              float4_t t[kBatch][2 * NT];
 #pragma unroll
-            for (int tt = 0; tt < NT; ++tt)
+              for (int i = 0; i < kBatch; ++i) {
+                const float4_t* theirs = slots4 + (size_t)(min(c0 + i, q_last) * kGroupWaves + wave) * kChunks;
 #pragma unroll
-              for (int h = 0; h < 2; ++h) acc[tt][h] += load16_coherent(theirs + (2 * tt + h) * 64 + lane);
-            // leave the workspace as found (zero): the other kernels sharing it
-            // take any non-zero slot word for a written partial
+                for (int h = 0; h < 2 * NT; ++h) t[i][h] = load16_coherent(theirs + h * 64 + lane);
+              }
 #pragma unroll
-            for (int tt = 0; tt < NT; ++tt)
+              for (int i = 0; i < kBatch; ++i)
+                if (c0 + i <= q_last) {
 #pragma unroll
-              for (int h = 0; h < 2; ++h)
-                store16_coherent(theirs + (2 * tt + h) * 64 + lane, float4_t{0.f, 0.f, 0.f, 0.f});
+                  for (int tt = 0; tt < NT; ++tt)
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) acc[tt][h] += t[i][2 * tt + h];
+                }
+#pragma unroll
+              for (int i = 0; i < kBatch; ++i) {
+                float4_t* theirs = slots4 + (size_t)(min(c0 + i, q_last) * kGroupWaves + wave) * kChunks;
+#pragma unroll
+                for (int h = 0; h < 2 * NT; ++h) store16_coherent(theirs + h * 64 + lane, float4_t{0.f, 0.f, 0.f, 0.f});
+              }
+            }
           }
         }
       }
@@ -878,13 +1172,13 @@ __global__ void __launch_bounds__(kGroupWaves * 64) int4_gemm_strip_groups_kerne
     };
     run_units(0, kb);
     if (kb < kmax) {
-      flush();
+      flush(FlushTag<false>{});
       ++gcur;
       part_end = min(hi, part_end + U);
       run_units(kb, kmax);
     }
   }
-  if (hi > lo) flush();  // the last part
+  if (hi > lo) flush(FlushTag<true>{});  // the last part
 }
 
 constexpr size_t kGroupMaxLds = 156 * 1024;

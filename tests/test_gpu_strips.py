@@ -3,8 +3,9 @@ byte-level restatement, and the strip GEMM against the oracle (dequantize the
 row-order stream, float32 matmul) within 1e-3 of the output RMS -- every
 plan shape (one whole strip per workgroup, strips shared by several
 workgroups, ranges over several strips), N from 1 to 32 (the strip kernel
-up to 8 rows, the strip-group kernel beyond), every ring depth, wave count
-and forced workgroup counts -- plus determinism, GEMM(N)
+up to 8 rows, the wide strip kernel beyond; on request the strip-group
+kernel or 8-row launches), every ring depth, wave count and forced
+workgroup counts -- plus determinism, GEMM(N)
 against stacked single-row products, and a workspace shared with the
 row-order kernels."""
 
@@ -103,13 +104,37 @@ def test_strip_gemm_forced_plans(K, M):
                     assert rel_err(y.cpu().numpy(), yref) <= TOL, (K, M, N, splits, depth, waves)
 
 
+@pytest.mark.parametrize("K,M", [(2048, 2048), (3072, 8192), (2048, 1056), (2048, 5504), (5632, 2048)])
+def test_strip_wide_gemm_forced_plans(K, M):
+    """N > 8 runs the wide strip kernel (all rows in one launch, one or two
+    16-row tiles): the automatic plan and workgroup counts that make ranges
+    start and end anywhere in a strip (several workgroups per strip, ranges
+    over several strips, one workgroup for everything)."""
+    from moat_amd.dequant import batched_int4_matmul, records_to_strips
+    blob, wdq = problem(K, M, 17 + K + M)
+    strips = records_to_strips(torch.from_numpy(blob).cuda(), K, M)
+    total = (M // 32) * (K // 32)
+    for N in (9, 16, 17, 24, 32):
+        x = O.synthetic_activations(N, K, 170 + N)
+        yref = x.astype(np.float32) @ wdq
+        xd = torch.from_numpy(x).cuda()
+        for splits in (0, 1, 2, 3, 7, 33, 100, 255, 256):
+            if splits > total:
+                continue
+            say(f"case: wide strip gemm K={K} M={M} N={N} workgroups={splits}")
+            y = batched_int4_matmul(xd, strips, K, M, strip_order=True, splits=splits)
+            assert rel_err(y.cpu().numpy(), yref) <= TOL, (K, M, N, splits)
+        say(f"case: strip gemm K={K} M={M} N={N} as 8-row launches")
+        y = batched_int4_matmul(xd, strips, K, M, strip_order=True, group=2)
+        assert rel_err(y.cpu().numpy(), yref) <= TOL, (K, M, N, "slices")
+
+
 @pytest.mark.parametrize("K,M", [(2048, 2048), (3072, 8192), (2048, 1056)])
 def test_strip_group_gemm_forced_plans(K, M):
-    """N > 8 runs the strip-group kernel (8 strips a group, one launch; 9..16
-    rows of matrices under 2^26 weights run as two strip-kernel launches, so
-    the two smaller shapes here reach the group kernel at N = 17 and 32):
-    workgroup counts that split groups anywhere, a partial last group (M/32
-    not a multiple of 8), both ring depths, one and two 16-row tiles."""
+    """On request (group=1) N > 8 runs the strip-group kernel (8 strips a
+    group, one launch): workgroup counts that split groups anywhere, a
+    partial last group (M/32 not a multiple of 8), both ring depths, one and
+    two 16-row tiles."""
     from moat_amd.dequant import batched_int4_matmul, records_to_strips
     blob, wdq = problem(K, M, 13 + K + M)
     strips = records_to_strips(torch.from_numpy(blob).cuda(), K, M)
@@ -123,7 +148,7 @@ def test_strip_group_gemm_forced_plans(K, M):
                 continue
             for depth in (2, 3):
                 say(f"case: strip group gemm K={K} M={M} N={N} workgroups={splits} depth={depth}")
-                y = batched_int4_matmul(xd, strips, K, M, strip_order=True, splits=splits, batch=depth)
+                y = batched_int4_matmul(xd, strips, K, M, strip_order=True, splits=splits, batch=depth, group=1)
                 assert rel_err(y.cpu().numpy(), yref) <= TOL, (K, M, N, splits, depth)
 
 
@@ -154,16 +179,18 @@ def test_strip_gemm_shares_the_workspace_with_row_order_calls():
         yref = x.astype(np.float32) @ wdq
         xd = torch.from_numpy(x).cuda()
         for rep in range(3):
-            for kind in ("strips", "records", "groups", "strips64", "general", "groups64", "strips"):
+            for kind in ("strips", "records", "groups", "strips64", "wide", "general", "groups64", "wide64",
+                         "strips"):
                 say(f"case: shared workspace N={N} rep={rep} {kind}")
                 if kind == "strips":
                     y = batched_int4_matmul(xd, strips, K, M, strip_order=True)
                 elif kind == "strips64":
                     y = batched_int4_matmul(xd, strips, K, M, strip_order=True, splits=64)
-                elif kind in ("groups", "groups64"):  # 16 rows (the strip-group kernel), first N compared
+                elif kind in ("groups", "groups64", "wide", "wide64"):  # 16 rows, first N compared
                     x16 = torch.cat([xd, xd.new_zeros((16 - N, K))]) if N < 16 else xd
                     y = batched_int4_matmul(x16, strips, K, M, strip_order=True,
-                                            splits=64 if kind == "groups64" else 0)[:N]
+                                            splits=64 if kind.endswith("64") else 0,
+                                            group=1 if kind.startswith("groups") else 0)[:N]
                 elif kind == "records":
                     y = batched_int4_matmul(xd, blob_d, K, M, algo=L.GEMM_MFMA, splits=8, front=L.FRONT_RECORDS)
                 else:
