@@ -3,19 +3,21 @@
 
 Workload (default): the FFN projection K=3072 x M=8192, weights ~N(0, 0.02)
 (seed 1003) quantized to 144-byte superblocks (3072*8192/256 = 98,304
-records, 14.16 MB), fp16 activations ~N(0, 1), swept over N = 1, 2, 4, 8,
-16, 32 parallel traces.  One "step" is one sweep: six projections, one per
-N, each on a different copy of the weight stream (copies rotate so that the
-256 MB Infinity Cache cannot serve repeats: >= 300 MB of distinct records).
-Beside it, the largest single-GPU projection, K=8192 x M=28672 (132 MB of
-records, 0.1 % outliers at 8 sigma), at N = 1, 8, 32 in tile order (the
-loader's layout) and row order (the reference's stream).
+records, 14.16 MB) and stored in strip order (the loader's layout for such
+shapes; --row-order: the reference's row-order stream), fp16 activations
+~N(0, 1), swept over N = 1, 2, 4, 8, 16, 32 parallel traces.  One "step" is
+one sweep: six projections, one per N, each on a different copy of the
+weight stream (copies rotate so that the 256 MB Infinity Cache cannot serve
+repeats: >= 300 MB of distinct records).  Beside it, the largest single-GPU
+projection, K=8192 x M=28672 (132 MB of records, 0.1 % outliers at 8 sigma),
+at N = 1, 8, 32 in strip, tile and row order.
 
 Printed: one JSON line with the whole-job throughput (tokens/s over the
-sweep), per-N microseconds per call (graph replay) and kernel time (HIP
-events around each call), HBM GB/s and roofline fraction on the kernel time,
-the same bytes read by a plain streaming-read kernel (the floor), the
-roofline of the dominant kernel and the CPU baseline (the numpy oracle of
+sweep), per-N microseconds per call (HIP-graph replay of back-to-back calls,
+HIP events on the launch stream), HBM GB/s and roofline fraction on that
+time, the same bytes read by a plain streaming-read kernel (the floor), the
+roofline of the dominant call (with the HBM traffic that rocprofv3 counted
+for it, when profiles/ holds it) and the CPU baseline (the numpy oracle of
 the reference CPU path on the host cores, with matmul-only, torch and
 one-thread variants).
 """
@@ -159,7 +161,7 @@ def traffic_from_counters(fetch_csv: str, write_csv: str, config: str, n: int) -
     fix-up kernel).  Each counter is scaled by what it reads for the largest
     plain copy of the same run: the clones of the weight stream, whose size is
     known (every clone reads and writes exactly the record bytes).  Returns
-    the entry written to profiles/traffic_<config>.json."""
+    the entry written to profiles/traffic_<config>_<layout>.json."""
     import csv
     K, M = CONFIGS[config][:2]
     sb_bytes = 144 * K * M // 256
@@ -352,8 +354,11 @@ def main() -> int:
                     help="GEMM configs: weights stored in tile order (each 256-column tile's rows contiguous; "
                          "moat_int4_records_to_tiles), read by moat_int4_gemm_tiles; needs M %% 256 == 0")
     ap.add_argument("--strip-order", action="store_true",
-                    help="GEMM configs: weights stored in strip order (moat_int4_records_to_strips), read by "
-                         "moat_int4_gemm_strips; needs K >= 2048")
+                    help="GEMM configs: weights in strip order (moat_int4_records_to_strips), read by "
+                         "moat_int4_gemm_strips -- the default wherever the loader stores it (K >= 2048, "
+                         "K %% 32 == 0, M %% 32 == 0)")
+    ap.add_argument("--row-order", action="store_true",
+                    help="GEMM configs: weights in the reference's row order, read by moat_int4_gemm_ex")
     ap.add_argument("--fused", action="store_true",
                     help="layer_h2048: Q, K, V in one launch and gate/up fused with SwiGLU (h feeds down)")
     ap.add_argument("--driver", action="store_true",
@@ -361,13 +366,18 @@ def main() -> int:
                          "each one launch, SwiGLU kernel, one graph over consecutive layers)")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"), default=None,
                     help="no GPU run: turn two rocprofv3 --pmc counter CSVs (FETCH_SIZE, WRITE_SIZE) of "
-                         "`bench.py --ns N` into profiles/traffic_<config>.json")
+                         "`bench.py --ns N` into profiles/traffic_<config>_<layout>.json")
     args = ap.parse_args()
 
     if args.traffic_from:
         n = int(args.ns.split(",")[0]) if args.ns else max(CONFIGS[args.config][5])
+        K, M = CONFIGS[args.config][:2]
+        layout = "tile" if args.tile_order else ("row" if args.row_order or not (K >= 2048 and K % 32 == 0
+                                                                                   and M % 32 == 0) else "strip")
         entry = traffic_from_counters(args.traffic_from[0], args.traffic_from[1], args.config, n)
-        path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", f"traffic_{args.config}.json")
+        entry["layout"] = layout
+        path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                            f"traffic_{args.config}_{layout}.json")
         data = json.load(open(path)) if os.path.exists(path) else {}
         data[str(n)] = entry
         with open(path, "w") as f:
@@ -399,7 +409,16 @@ def main() -> int:
         return 2
     ns = [int(v) for v in args.ns.split(",")] if args.ns else CONFIGS[args.config][5]
     timer = Timer(torch)
-    layout = "strip" if args.strip_order else ("tile" if args.tile_order else "row")
+    strip_ok = K >= 2048 and K % 32 == 0 and M % 32 == 0  # the loader's strip_layout_ok
+    if args.tile_order:
+        layout = "tile"
+    elif args.row_order or not strip_ok:
+        if args.strip_order:
+            print(f"--strip-order needs K >= 2048, K %% 32 == 0 and M %% 32 == 0 (K = {K}, M = {M})", file=sys.stderr)
+            return 2
+        layout = "row"
+    else:
+        layout = "strip"
     main_res = measure_projection(torch, timer, lib, args.config, ns, layout, args)
     per_n, call = main_res["per_n"], main_res["call"]
     copies = main_res["copies"]
@@ -446,14 +465,15 @@ def main() -> int:
                    f"call / {per_n[dom]['us_per_call']} us per call (HIP-graph replay of back-to-back calls; the "
                    f"main kernel plus the fix-up kernel when the plan has one)"),
     }
-    traffic_file = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
-                                f"traffic_{args.config}.json")
-    if os.path.exists(traffic_file) and layout == "row":
+    traffic_name = f"traffic_{args.config}_{layout}.json"
+    traffic_file = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", traffic_name)
+    if os.path.exists(traffic_file):
         with open(traffic_file) as f:
             tr = json.load(f).get(str(dom))
         if tr is not None:
             roof["traffic"] = tr["traffic"]
-            roof["traffic_source"] = f"profiles/traffic_{args.config}.json (all kernels of the call)"
+            roof["traffic_over_algorithmic"] = tr["traffic_over_algorithmic"]
+            roof["traffic_source"] = f"profiles/{traffic_name} (rocprofv3 FETCH_SIZE + WRITE_SIZE, all kernels of the call)"
 
     cpu = None
     if not args.no_cpu_baseline:

@@ -126,24 +126,22 @@ __device__ __forceinline__ void load8_sc1(float4_t (&t)[8], const float* base, c
       : "memory");
 }
 
-// 16-byte device-coherent accesses (two agent-scope 8-byte atomics, sc1)
-// that the compiler schedules and waits for itself.
-__device__ __forceinline__ float4_t load16_coherent(const float4_t* p) {
-  const unsigned long long* q = reinterpret_cast<const unsigned long long*>(p);
-  const unsigned long long a = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  const unsigned long long b = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  return float4_t{__builtin_bit_cast(float, (uint32_t)a), __builtin_bit_cast(float, (uint32_t)(a >> 32)),
-                  __builtin_bit_cast(float, (uint32_t)b), __builtin_bit_cast(float, (uint32_t)(b >> 32))};
+// 16-byte device-coherent (sc1) buffer accesses through the compiler, which
+// schedules them, waits for the loads and keeps the matrix-core hazards of
+// their operands (inline assembly would hide an accumulator's pending write
+// from it); one 16-byte access a lane writes whole cache lines a wave.
+typedef unsigned int u32x4_t __attribute__((__vector_size__(16)));
+constexpr int kCpolSc1 = 16;  // cache-policy bit SC1 of a buffer access
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t coherent_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7FFFFFFF, 0x00020000);
 }
-// (The elements go through __float_as_uint: this compiler evaluates
-// __builtin_bit_cast applied directly to a vector element as element 0.)
-__device__ __forceinline__ void store16_coherent(float4_t* p, float4_t v) {
-  unsigned long long* q = reinterpret_cast<unsigned long long*>(p);
-  const unsigned long long a = (unsigned long long)__float_as_uint(v[0]) | ((unsigned long long)__float_as_uint(v[1]) << 32);
-  const unsigned long long b = (unsigned long long)__float_as_uint(v[2]) | ((unsigned long long)__float_as_uint(v[3]) << 32);
-  __hip_atomic_store(q, a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __hip_atomic_store(q + 1, b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ void store16_sc1(__amdgpu_buffer_rsrc_t r, uint32_t off, float4_t v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), r, (int)off, 0, kCpolSc1);
 }
+__device__ __forceinline__ float4_t load16_sc1(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, kCpolSc1));
+}
+// A 16-byte device-coherent load as two agent-scope 8-byte atomics (sc1).
 __device__ __forceinline__ float4_t load16_coherent(const float* base, uint32_t byte_off) {
   const unsigned long long* q = reinterpret_cast<const unsigned long long*>(reinterpret_cast<const uint8_t*>(base) + byte_off);
   const unsigned long long a = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1002,19 +1000,23 @@ __global__ void __launch_bounds__(kGroupWaves * 64) int4_gemm_strip_groups_kerne
     const int a = max(lo, gcur * U), b = min(hi, (gcur + 1) * U);
     const bool whole = a == gcur * U && b == (gcur + 1) * U;
     const bool owner = !whole && a == gcur * U;
-    float4_t* slots4 = reinterpret_cast<float4_t*>(P.slots);
+    const __amdgpu_buffer_rsrc_t srs = coherent_rsrc(P.slots);
     uint32_t* flags = P.status + kWsStatusBytes / 4;  // one word per workgroup, zero between calls
     constexpr int kChunks = NT * 2 * 64;               // float4 chunks of one wave's sums
+    // byte offset of chunk h of the sums of workgroup c's wave
+    auto slot_off = [&](int c, int h) { return (uint32_t)(16 * ((c * kGroupWaves + wave) * kChunks + h * 64 + lane)); };
     if (!whole && !owner) {  // the first part of the range: stored for the group's first workgroup
       if (strip < P.strips) {
-        float4_t* mine = slots4 + (size_t)(p * kGroupWaves + wave) * kChunks;
 #pragma unroll
         for (int tt = 0; tt < NT; ++tt)
 #pragma unroll
-          for (int h = 0; h < 2; ++h) store16_coherent(mine + (2 * tt + h) * 64 + lane, acc[tt][h]);
+          for (int h = 0; h < 2; ++h) store16_sc1(srs, slot_off(p, 2 * tt + h), acc[tt][h]);
       }
-      // the sums are device-coherent stores: complete (vmcnt counts stores)
-      // in every wave before wave 0 raises the flag
+      asm volatile("" ::: "memory");
+      // the sums go out as 16-byte device-coherent stores (whole lines a
+      // wave, where two 8-byte atomics a lane would write each line twice),
+      // complete (vmcnt counts stores) in every wave before wave 0 raises
+      // the flag
       wait_vmcnt<0>();
       lds_barrier();
       if (wave == 0) __hip_atomic_store(flags + p, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1055,11 +1057,10 @@ __global__ void __launch_bounds__(kGroupWaves * 64) int4_gemm_strip_groups_kerne
             for (int c0 = p + 1; c0 <= q_last; c0 += kBatch) {
               float4_t t[kBatch][2 * NT];
 #pragma unroll
-              for (int i = 0; i < kBatch; ++i) {
-                const float4_t* theirs = slots4 + (size_t)(min(c0 + i, q_last) * kGroupWaves + wave) * kChunks;
+              for (int i = 0; i < kBatch; ++i)
 #pragma unroll
-                for (int h = 0; h < 2 * NT; ++h) t[i][h] = load16_coherent(theirs + h * 64 + lane);
-              }
+                for (int h = 0; h < 2 * NT; ++h) t[i][h] = load16_sc1(srs, slot_off(min(c0 + i, q_last), h));
+              wait_vmcnt<0>();  // every load has read its slot before the slots are cleared
 #pragma unroll
               for (int i = 0; i < kBatch; ++i)
                 if (c0 + i <= q_last) {
@@ -1069,11 +1070,10 @@ __global__ void __launch_bounds__(kGroupWaves * 64) int4_gemm_strip_groups_kerne
                     for (int h = 0; h < 2; ++h) acc[tt][h] += t[i][2 * tt + h];
                 }
 #pragma unroll
-              for (int i = 0; i < kBatch; ++i) {
-                float4_t* theirs = slots4 + (size_t)(min(c0 + i, q_last) * kGroupWaves + wave) * kChunks;
+              for (int i = 0; i < kBatch; ++i)
 #pragma unroll
-                for (int h = 0; h < 2 * NT; ++h) store16_coherent(theirs + h * 64 + lane, float4_t{0.f, 0.f, 0.f, 0.f});
-              }
+                for (int h = 0; h < 2 * NT; ++h)
+                  store16_sc1(srs, slot_off(min(c0 + i, q_last), h), float4_t{0.f, 0.f, 0.f, 0.f});
             }
           }
         }
