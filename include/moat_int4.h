@@ -215,7 +215,9 @@ int32_t moat_int4_gemm_tiles(const uint16_t* x_f16, const uint8_t* tiles, float*
  * shares the status word), sized by moat_int4_gemm_strips_workspace_size;
  * options: `splits` = workgroups (0 automatic), `group` = kernel (0
  * automatic; 1 the strip-group kernel for N > 8; 2 the strip kernel, 8 rows
- * a launch; 3 the wide strip kernel), `batch` = ring depth of the strip
+ * a launch; 3 the wide strip kernel), `algo` = MOAT_GEMM_DOT2 for the
+ * strip kernel's vector-ALU variant (v_dot2_f32_f16 and a reduction across
+ * lanes; N <= 4, MOAT_ERR_INVALID beyond), `batch` = ring depth of the strip
  * kernel (2..4) or the strip-group kernel (2 or 3), 0 automatic, `waves` =
  * waves per workgroup of the strip kernel (4, 8 or 12; 0 automatic), the
  * rest ignored.

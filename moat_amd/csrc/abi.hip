@@ -52,7 +52,7 @@ hipError_t launch_records_to_tiles(const uint8_t* sb, int k, int m, uint8_t* til
 hipError_t launch_swiglu_f32(const float* gu, int n, int m, int64_t ld, uint16_t* h, hipStream_t stream);
 hipError_t launch_stream_read(const void* src, int64_t bytes, uint32_t* sink, int blocks, hipStream_t st);
 hipError_t launch_gemm_strips(const uint16_t* x, const uint8_t* w, float* y, int n, int k, int m, int wgs, int depth,
-                              int waves, float* slots, uint32_t* status, hipStream_t stream);
+                              int waves, bool dot, float* slots, uint32_t* status, hipStream_t stream);
 hipError_t launch_records_to_strips(const uint8_t* sb, int k, int m, uint8_t* strips, hipStream_t stream);
 hipError_t launch_strips_to_records(const uint8_t* strips, int k, int m, uint8_t* sb, hipStream_t stream);
 int strips_waves(int n, int waves);
@@ -424,6 +424,7 @@ bool strips_shape_ok(int32_t n, int32_t k, int32_t m) {
 
 struct StripPlan {
   int kind;  // kStripSlices, kStripGroups or kStripWide
+  bool dot;  // the strip kernel's v_dot2 variant (options algo = MOAT_GEMM_DOT2, N <= 4)
   int wgs;
   int depth;
   int waves;
@@ -436,7 +437,8 @@ constexpr int kStripSlices = 0, kStripGroups = 1, kStripWide = 2;
 
 bool strip_options_ok(const moat_int4_gemm_options* o) {
   return !o || (o->splits >= 0 && o->batch >= 0 && (o->waves == 0 || o->waves == 4 || o->waves == 8 || o->waves == 12) &&
-                o->group >= 0 && o->group <= 3);
+                o->group >= 0 && o->group <= 3 &&
+                (o->algo == MOAT_GEMM_AUTO || o->algo == MOAT_GEMM_MFMA || o->algo == MOAT_GEMM_DOT2));
 }
 
 // The strip kernel: workgroups, one whole strip each when M/32 is
@@ -453,6 +455,24 @@ StripPlan plan_strips(int32_t n, int32_t k, int32_t m, const moat_int4_gemm_opti
   StripPlan p;
   const int64_t strips = m / 32, units = k / 32;
   const int forced = o ? o->group : 0;
+  p.dot = o && o->algo == MOAT_GEMM_DOT2;
+  if (p.dot) {  // the strip kernel's VALU variant: N <= 4 only
+    p.kind = kStripSlices;
+    const int64_t total = strips * units;
+    int64_t wgs;
+    if (o->splits > 0) wgs = o->splits < kStripMaxWorkgroups ? o->splits : kStripMaxWorkgroups;
+    else if (strips >= 128 && strips <= 256) wgs = strips;
+    else wgs = total / 16 < 256 ? (total / 16 > 0 ? total / 16 : 1) : 256;
+    if (wgs > total) wgs = total;
+    p.wgs = (int)wgs;
+    const int waves = o->waves ? o->waves : (total / wgs <= 256 ? 12 : 8);
+    p.waves = moat::strips_waves(n, waves);
+    p.depth = 2;
+    const int64_t base = total / wgs, rem = total % wgs;
+    const bool shared = !(rem == 0 && base % units == 0);
+    p.workspace_bytes = shared ? kCounterBlockBytes + wgs * kStripRowsPerLaunch * 32 * (int64_t)sizeof(float) : 0;
+    return p;
+  }
   const bool groups_fit = strips * units * 576 < ((int64_t)1 << 32);
   const int64_t weights = (int64_t)k * m;
   p.kind = kStripSlices;
@@ -581,14 +601,16 @@ int32_t moat_int4_strips_to_records(const uint8_t* strips, int32_t k, int32_t m,
 
 int64_t moat_int4_gemm_strips_workspace_size(int32_t n, int32_t k, int32_t m,
                                              const moat_int4_gemm_options* options) {
-  if (!strips_shape_ok(n, k, m) || !strip_options_ok(options)) return -1;
+  if (!strips_shape_ok(n, k, m) || !strip_options_ok(options) || (options && options->algo == MOAT_GEMM_DOT2 && n > 4))
+    return -1;
   return plan_strips(n, k, m, options).workspace_bytes;
 }
 
 int32_t moat_int4_gemm_strips(const uint16_t* x_f16, const uint8_t* strips, float* y_f32, int32_t n, int32_t k,
                               int32_t m, const moat_int4_gemm_options* options, void* workspace,
                               int64_t workspace_bytes, hipStream_t stream) {
-  if (!strips_shape_ok(n, k, m) || !strip_options_ok(options)) return MOAT_ERR_INVALID;
+  if (!strips_shape_ok(n, k, m) || !strip_options_ok(options) || (options && options->algo == MOAT_GEMM_DOT2 && n > 4))
+    return MOAT_ERR_INVALID;
   if (!x_f16 || !strips || !y_f32 || !aligned(x_f16, 16) || !aligned(strips, 16) || !aligned(y_f32, 4))
     return MOAT_ERR_INVALID;
   const StripPlan p = plan_strips(n, k, m, options);
@@ -608,7 +630,7 @@ int32_t moat_int4_gemm_strips(const uint16_t* x_f16, const uint8_t* strips, floa
   for (int32_t r0 = 0; r0 < n; r0 += kStripRowsPerLaunch) {
     const int32_t rows = n - r0 < kStripRowsPerLaunch ? n - r0 : kStripRowsPerLaunch;
     const hipError_t e = moat::launch_gemm_strips(x_f16 + (int64_t)r0 * k, strips, y_f32 + (int64_t)r0 * m, rows,
-                                                  k, m, p.wgs, p.depth, p.waves, slots, status, stream);
+                                                  k, m, p.wgs, p.depth, p.waves, p.dot, slots, status, stream);
     if (e != hipSuccess) return MOAT_ERR_HIP;
   }
   return MOAT_OK;

@@ -240,8 +240,22 @@ __device__ __forceinline__ void strip_part_out(const StripParams& P, const float
   }
 }
 
-template <int NX, int kDepth, int W>
+// acc + sum of x[i] * w[i] over 8 fp16 pairs, four v_dot2_f32_f16.
+__device__ __forceinline__ float dot8_f16(half8_t x, half8_t w, float acc) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    acc = __builtin_amdgcn_fdot2(half2_t{x[2 * i], x[2 * i + 1]}, half2_t{w[2 * i], w[2 * i + 1]}, acc, false);
+  return acc;
+}
+
+// kDot: the same walk with the products on the vector ALUs instead of the
+// matrix cores (v_dot2_f32_f16; lane (q, j) keeps the sums of columns 2j,
+// 2j+1 over rows 8q..8q+7 of each unit for every row of X, reduced across
+// the four q lanes at a part's end) -- the wavefront-reduction GEMV, kept
+// to measure against the matrix-core path for N <= 4.
+template <int NX, int kDepth, int W, bool kDot = false>
 __global__ void __launch_bounds__(W * 64) int4_gemm_strips_kernel(StripParams P) {
+  static_assert(!kDot || NX <= 4, "the dot2 variant stages at most 4 rows");
   using G = StripGeom<NX, W>;
   constexpr int kSU = G::kStageUnits;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -282,6 +296,9 @@ __global__ void __launch_bounds__(W * 64) int4_gemm_strips_kernel(StripParams P)
   const uint32_t rsc = 144 * q, rpay = 144 * q + 16 + 8 * j;
   const int xrow = min(j, P.n - 1);
   const uint32_t rx = (uint32_t)(G::kXRowBytes * xrow + 16 * (q ^ ((xrow >> 2) & 3)));
+  uint32_t rxd[NX];  // kDot: quarter q of every staged row
+#pragma unroll
+  for (int n = 0; n < NX; ++n) rxd[n] = (uint32_t)(G::kXRowBytes * n + 16 * (q ^ ((n >> 2) & 3)));
 
   uint8_t* wring = smem + wave * G::template wave_bytes<kDepth>();
   uint8_t* xring = wring + kDepth * G::kWStage;
@@ -364,10 +381,25 @@ __global__ void __launch_bounds__(W * 64) int4_gemm_strips_kernel(StripParams P)
   };
 
   float4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+  float dacc[NX][2] = {};  // kDot: row n, columns 2j and 2j+1, rows 8q..8q+7 of the units
 
   auto flush = [&](int pi) {
     float* sl = slots + ((pi & 1) * W + wave) * NX * kStripCols;
-    if (q < 2) {
+    if constexpr (kDot) {
+#pragma unroll
+      for (int n = 0; n < NX; ++n)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {  // the four q lanes of column pair j, in q order
+          const float v0 = dacc[n][c], v1 = __shfl_xor(v0, 16), v2 = __shfl_xor(v0, 32), v3 = __shfl_xor(v0, 48);
+          dacc[n][c] = q == 0 ? (v0 + v1) + (v2 + v3) : 0.f;
+        }
+      if (q == 0) {
+#pragma unroll
+        for (int n = 0; n < NX; ++n) *reinterpret_cast<float2*>(sl + n * kStripCols + 2 * j) = float2{dacc[n][0], dacc[n][1]};
+      }
+#pragma unroll
+      for (int n = 0; n < NX; ++n) dacc[n][0] = dacc[n][1] = 0.f;
+    } else if (q < 2) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int r = 4 * q + v;
@@ -392,12 +424,17 @@ __global__ void __launch_bounds__(W * 64) int4_gemm_strips_kernel(StripParams P)
   // pair j), then its arithmetic: the reads of a batch of units go out before
   // the first unit's arithmetic.
   struct UnitRegs {
-    half8_t a;
+    half8_t a[kDot ? NX : 1];
     uint4 sc;
     uint2 b;
   };
   auto load_unit = [&](UnitRegs& r, const uint8_t* wu, const uint8_t* xu) {
-    r.a = *reinterpret_cast<const half8_t*>(xu + rx);
+    if constexpr (kDot) {
+#pragma unroll
+      for (int n = 0; n < NX; ++n) r.a[n] = *reinterpret_cast<const half8_t*>(xu + rxd[n]);
+    } else {
+      r.a[0] = *reinterpret_cast<const half8_t*>(xu + rx);
+    }
     r.sc = *reinterpret_cast<const uint4*>(wu + rsc);
     r.b = *reinterpret_cast<const uint2*>(wu + rpay);
   };
@@ -422,8 +459,16 @@ __global__ void __launch_bounds__(W * 64) int4_gemm_strips_kernel(StripParams P)
       b1[2 * pp] = hi2[pp][0];
       b1[2 * pp + 1] = hi2[pp][1];
     }
-    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(r.a, b0, acc0, 0, 0, 0);
-    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(r.a, b1, acc1, 0, 0, 0);
+    if constexpr (kDot) {
+#pragma unroll
+      for (int n = 0; n < NX; ++n) {
+        dacc[n][0] = dot8_f16(r.a[n], b0, dacc[n][0]);
+        dacc[n][1] = dot8_f16(r.a[n], b1, dacc[n][1]);
+      }
+    } else {
+      acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(r.a[0], b0, acc0, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(r.a[0], b1, acc1, 0, 0, 0);
+    }
   };
   auto compute = [&](const uint8_t* wu, const uint8_t* xu) {
     UnitRegs r;
@@ -488,11 +533,11 @@ __global__ void __launch_bounds__(W * 64) int4_gemm_strips_kernel(StripParams P)
 
 constexpr size_t kStripMaxLds = 156 * 1024;
 
-template <int NX, int kDepth, int W>
+template <int NX, int kDepth, int W, bool kDot = false>
 static hipError_t launch_strips_one(const StripParams& P, int wgs, hipStream_t stream) {
   const size_t lds = StripGeom<NX, W>::template lds_bytes<kDepth>();
   if (lds > kStripMaxLds) return hipErrorInvalidValue;  // never launch past the LDS
-  hipLaunchKernelGGL((int4_gemm_strips_kernel<NX, kDepth, W>), dim3(wgs), dim3(W * 64), lds, stream, P);
+  hipLaunchKernelGGL((int4_gemm_strips_kernel<NX, kDepth, W, kDot>), dim3(wgs), dim3(W * 64), lds, stream, P);
   return hipGetLastError();
 }
 
@@ -537,8 +582,9 @@ static hipError_t launch_strips_w(const StripParams& P, int wgs, int depth, hipS
   return launch_strips_one<NX, 2, W>(P, wgs, stream);
 }
 
+// dot: the v_dot2 variant (n <= 4, ring depth 2).
 hipError_t launch_gemm_strips(const uint16_t* x, const uint8_t* w, float* y, int n, int k, int m, int wgs, int depth,
-                              int waves, float* slots, uint32_t* status, hipStream_t stream) {
+                              int waves, bool dot, float* slots, uint32_t* status, hipStream_t stream) {
   StripParams P = {};
   P.x = x; P.w = w; P.y = y; P.slots = slots; P.status = status;
   P.n = n; P.k = k; P.m = m;
@@ -550,6 +596,17 @@ hipError_t launch_gemm_strips(const uint16_t* x, const uint8_t* w, float* y, int
   const int nx = strips_rows_staged(n);
   waves = strips_waves(n, waves);
   depth = strips_depth(n, waves, depth);
+  if (dot) {
+    if (nx > 4) return hipErrorInvalidValue;
+    if (waves == 12)
+      return nx == 1 ? launch_strips_one<1, 2, 12, true>(P, wgs, stream)
+             : nx == 2 ? launch_strips_one<2, 2, 12, true>(P, wgs, stream) : launch_strips_one<4, 2, 12, true>(P, wgs, stream);
+    if (waves == 8)
+      return nx == 1 ? launch_strips_one<1, 2, 8, true>(P, wgs, stream)
+             : nx == 2 ? launch_strips_one<2, 2, 8, true>(P, wgs, stream) : launch_strips_one<4, 2, 8, true>(P, wgs, stream);
+    return nx == 1 ? launch_strips_one<1, 2, 4, true>(P, wgs, stream)
+           : nx == 2 ? launch_strips_one<2, 2, 4, true>(P, wgs, stream) : launch_strips_one<4, 2, 4, true>(P, wgs, stream);
+  }
   if (waves == 12) {
     if (nx == 1) return launch_strips_w<1, 12>(P, wgs, depth, stream);
     if (nx == 2) return launch_strips_w<2, 12>(P, wgs, depth, stream);

@@ -129,6 +129,34 @@ def test_strip_wide_gemm_forced_plans(K, M):
         assert rel_err(y.cpu().numpy(), yref) <= TOL, (K, M, N, "slices")
 
 
+@pytest.mark.parametrize("K,M", [(2048, 2048), (3072, 8192), (2048, 1056), (2048, 32000)])
+def test_strip_dot2_variant_matches_oracle(K, M):
+    """The strip kernel's vector-ALU variant (algo=MOAT_GEMM_DOT2: v_dot2 and
+    a reduction across the four lanes of a column pair), N = 1..4, with the
+    automatic and forced workgroup counts and every wave count; N = 5 is
+    refused."""
+    from moat_amd import _lib as L
+    from moat_amd.dequant import batched_int4_matmul, records_to_strips
+    blob, wdq = problem(K, M, 19 + K + M)
+    strips = records_to_strips(torch.from_numpy(blob).cuda(), K, M)
+    total = (M // 32) * (K // 32)
+    for N in (1, 2, 3, 4):
+        x = O.synthetic_activations(N, K, 190 + N)
+        yref = x.astype(np.float32) @ wdq
+        xd = torch.from_numpy(x).cuda()
+        for splits in (0, 1, 7, 100, 256):
+            for waves in (0, 4, 8, 12):
+                if splits > total:
+                    continue
+                say(f"case: dot2 strip gemm K={K} M={M} N={N} workgroups={splits} waves={waves}")
+                y = batched_int4_matmul(xd, strips, K, M, strip_order=True, algo=L.GEMM_DOT2, splits=splits,
+                                        waves=waves)
+                assert rel_err(y.cpu().numpy(), yref) <= TOL, (K, M, N, splits, waves)
+    with pytest.raises(ValueError):
+        batched_int4_matmul(torch.zeros((5, K), dtype=torch.float16, device="cuda"), strips, K, M, strip_order=True,
+                            algo=L.GEMM_DOT2)
+
+
 @pytest.mark.parametrize("K,M", [(2048, 2048), (3072, 8192), (2048, 1056)])
 def test_strip_group_gemm_forced_plans(K, M):
     """On request (group=1) N > 8 runs the strip-group kernel (8 strips a
