@@ -58,7 +58,7 @@ hipError_t launch_strips_to_records(const uint8_t* strips, int k, int m, uint8_t
 int strips_waves(int n, int waves);
 int strips_depth(int n, int waves, int depth);
 hipError_t launch_gemm_strips_wide(const uint16_t* x, const uint8_t* w, float* y, int n, int k, int m, int wgs,
-                                   float* slots, uint32_t* status, hipStream_t stream);
+                                   int su, int depth, float* slots, uint32_t* status, hipStream_t stream);
 hipError_t launch_gemm_strip_groups(const uint16_t* x, const uint8_t* w, float* y, int n, int k, int m, int wgs,
                                     int depth, float* slots, uint32_t* status, hipStream_t stream);
 int strip_groups_slot_bytes(int n);
@@ -425,6 +425,7 @@ bool strips_shape_ok(int32_t n, int32_t k, int32_t m) {
 struct StripPlan {
   int kind;  // kStripSlices, kStripGroups or kStripWide
   bool dot;  // the strip kernel's v_dot2 variant (options algo = MOAT_GEMM_DOT2, N <= 4)
+  int su;    // the wide strip kernel's units a stage (0: its default)
   int wgs;
   int depth;
   int waves;
@@ -437,7 +438,7 @@ constexpr int kStripSlices = 0, kStripGroups = 1, kStripWide = 2;
 
 bool strip_options_ok(const moat_int4_gemm_options* o) {
   return !o || (o->splits >= 0 && o->batch >= 0 && (o->waves == 0 || o->waves == 4 || o->waves == 8 || o->waves == 12) &&
-                o->group >= 0 && o->group <= 3 &&
+                o->group >= 0 && o->group <= 3 && (o->front == 0 || o->front == 1 || o->front == 2 || o->front == 4) &&
                 (o->algo == MOAT_GEMM_AUTO || o->algo == MOAT_GEMM_MFMA || o->algo == MOAT_GEMM_DOT2));
 }
 
@@ -452,7 +453,7 @@ bool strip_options_ok(const moat_int4_gemm_options* o) {
 // than 2^32 bytes (its copy offsets are 32-bit): up to 256 workgroups of at
 // least 16 items and slots of 8 waves x 2 or 4 KB per workgroup.
 StripPlan plan_strips(int32_t n, int32_t k, int32_t m, const moat_int4_gemm_options* o) {
-  StripPlan p;
+  StripPlan p = {};
   const int64_t strips = m / 32, units = k / 32;
   const int forced = o ? o->group : 0;
   p.dot = o && o->algo == MOAT_GEMM_DOT2;
@@ -511,9 +512,10 @@ StripPlan plan_strips(int32_t n, int32_t k, int32_t m, const moat_int4_gemm_opti
   p.wgs = (int)wgs;
   const int64_t base = total / wgs, rem = total % wgs;
   const bool shared = !(rem == 0 && base % units == 0);
-  if (p.kind == kStripWide) {  // 8 waves, a two-stage ring; slots of n x 32 floats
+  if (p.kind == kStripWide) {  // 8 waves; slots of n x 32 floats
     p.waves = 8;
-    p.depth = 2;
+    p.depth = o ? o->batch : 0;  // 0: two stages
+    p.su = o ? o->front : 0;
     p.workspace_bytes = shared ? kCounterBlockBytes + wgs * n * 32 * (int64_t)sizeof(float) : 0;
     return p;
   }
@@ -625,7 +627,8 @@ int32_t moat_int4_gemm_strips(const uint16_t* x_f16, const uint8_t* strips, floa
     return status_of(moat::launch_gemm_strip_groups(x_f16, strips, y_f32, n, k, m, p.wgs, p.depth, slots, status,
                                                     stream));
   if (p.kind == kStripWide)
-    return status_of(moat::launch_gemm_strips_wide(x_f16, strips, y_f32, n, k, m, p.wgs, slots, status, stream));
+    return status_of(moat::launch_gemm_strips_wide(x_f16, strips, y_f32, n, k, m, p.wgs, p.su, p.depth, slots, status,
+                                                   stream));
   // 8 rows of X per launch; the launches share the workspace in stream order
   for (int32_t r0 = 0; r0 < n; r0 += kStripRowsPerLaunch) {
     const int32_t rows = n - r0 < kStripRowsPerLaunch ? n - r0 : kStripRowsPerLaunch;

@@ -627,30 +627,36 @@ hipError_t launch_gemm_strips(const uint16_t* x, const uint8_t* w, float* y, int
 // ---------------------------------------------------------------------------
 // Wide strips: the strip kernel's walk for 9 <= N <= 32 in one launch.
 //  * the same unit ranges, stages, ring and hand-off as the strip kernel,
-//    with 8 waves and 16 or 32 rows of X (one or two 16-row MFMA tiles on
-//    the same decoded weights), so that a strip's weights are read once for
-//    all N rows and, where the plan gives each workgroup whole strips,
-//    nothing is handed between workgroups;
-//  * a wave's stage holds 4 (16 rows) or 2 (32 rows) units: its X is 4 KB,
-//    rows kRowChunks 16-byte chunks apart, copied as 4 copies of 1 KB that
-//    each cover 4 or 8 whole rows; chunk c of row r sits at position
-//    c ^ wide_swz(r) of its row, so that one quarter of 16 rows falls on 16
+//    with 8 waves and R = 8, 16 or 32 rows of X (one or two 16-row MFMA
+//    tiles on the same decoded weights; with 8 rows, lanes of tile rows 8..15
+//    read row 7 and their products are never stored), so that a strip's
+//    weights are read once for all N rows and, where the plan gives each
+//    workgroup whole strips, nothing is handed between workgroups;
+//  * a wave's stage holds SU = 1, 2 or 4 units: its X is R x SU x 64 bytes,
+//    rows kRowChunks = 4 SU
+//    16-byte chunks apart, copied as 1 KB copies that each cover 64 /
+//    kRowChunks whole rows; chunk c of row r sits at position c ^
+//    wide_swz(r) of its row, so that one quarter of 16 rows falls on 16
 //    different 16-byte bank groups;
 //  * at a strip boundary every wave leaves its sums in LDS, and 2 or 4 waves
 //    each reduce and write (or hand off) 8 rows of the part.
 constexpr int kWideWaves = 8;
 
-template <int NT>
+template <int R, int SU>
 struct WideGeom {
-  static constexpr int kRows = 16 * NT;                          // X rows staged (rows past N repeat row N - 1)
-  static constexpr int kStageUnits = NT == 1 ? 4 : 2;            // a wave's units a stage
-  static constexpr int kWChunks = 36 * kStageUnits;              // 144, 72
-  static constexpr int kWLoads = (kWChunks + 63) / 64;           // 3, 2
-  static constexpr int kWTail = kWChunks - 64 * (kWLoads - 1);   // lanes of the last weight copy: 16, 8
-  static constexpr int kWStage = 16 * kWChunks;                  // 2304, 1152
-  static constexpr int kRowChunks = 4 * kStageUnits;             // 16-byte chunks of a row's stage: 16, 8
-  static constexpr int kXStage = kRows * 16 * kRowChunks;        // 4096
-  static constexpr int kXLoads = kXStage / 1024;                 // 4
+  static_assert(SU == 1 || SU == 2 || SU == 4, "1, 2 or 4 units a stage");
+  static_assert(R == 8 || R == 16 || R == 32, "8, 16 or 32 rows");
+  static constexpr int kRows = R;                                // X rows staged (rows past N repeat row N - 1)
+  static constexpr int kTiles = (R + 15) / 16;                   // 16-row MFMA tiles
+  static constexpr int kStageUnits = SU;                         // a wave's units a stage
+  static constexpr int kWChunks = 36 * kStageUnits;              // 144, 72, 36
+  static constexpr int kWLoads = (kWChunks + 63) / 64;           // 3, 2, 1
+  static constexpr int kWTail = kWChunks - 64 * (kWLoads - 1);   // lanes of the last weight copy: 16, 8, 36
+  static constexpr int kWStage = 16 * kWChunks;                  // 2304, 1152, 576
+  static constexpr int kRowChunks = 4 * kStageUnits;             // 16-byte chunks of a row's stage: 16, 8, 4
+  static constexpr int kXStage = kRows * 16 * kRowChunks;
+  static constexpr int kXLoads = kXStage / 1024;
+  static_assert(kXStage % 1024 == 0, "whole 1 KB copies");
   static constexpr int kLS = kWLoads + kXLoads;                  // copies a stage
   static constexpr int kSlotBytes = kRows * kStripCols * 4;      // one wave's sums of a part
   static constexpr int kPasses = kRows / 8;                      // output waves of a part
@@ -662,12 +668,18 @@ struct WideGeom {
   }
 };
 
-template <int NT>
-__device__ __forceinline__ int wide_swz(int r) { return NT == 1 ? (r & 15) : ((r >> 1) & 7); }
+// Position swizzle of a row's chunks: rows r and r + 16 / kRowChunks apart
+// get different XOR patterns, so the 16 rows of a quarter spread over 16
+// bank groups (kRowChunks = 16, 8, 4: r & 15, (r >> 1) & 7, (r >> 2) & 3).
+template <int SU>
+__device__ __forceinline__ int wide_swz(int r) {
+  return SU == 4 ? (r & 15) : SU == 2 ? ((r >> 1) & 7) : ((r >> 2) & 3);
+}
 
-template <int NT, int kDepth>
+template <int R, int SU, int kDepth>
 __global__ void __launch_bounds__(kWideWaves * 64) int4_gemm_strips_wide_kernel(StripParams P) {
-  using G = WideGeom<NT>;
+  using G = WideGeom<R, SU>;
+  constexpr int NT = G::kTiles;
   constexpr int W = kWideWaves;
   constexpr int kSU = G::kStageUnits;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -702,19 +714,20 @@ __global__ void __launch_bounds__(kWideWaves * 64) int4_gemm_strips_wide_kernel(
   for (int i = 0; i < G::kXLoads; ++i) {
     const int pos = 64 * i + lane;
     const int r = pos / G::kRowChunks;
-    const int c = (pos % G::kRowChunks) ^ wide_swz<NT>(r);
+    const int c = (pos % G::kRowChunks) ^ wide_swz<SU>(r);
     xk[i] = c >> 2;
     xoff[i] = (uint32_t)(2 * (min(r, P.n - 1) * P.k + 8 * (c & 3)));
   }
   // LDS reads of unit k of a stage: record q's 8 row scales, the 8 bytes of
-  // column pair j, and quarter q of X row 16 tt + j
+  // column pair j, and quarter q of X row 16 tt + j (past the staged rows:
+  // the last one)
   const uint32_t rsc = 144 * q, rpay = 144 * q + 16 + 8 * j;
   uint32_t rx[NT][kSU];
 #pragma unroll
   for (int tt = 0; tt < NT; ++tt) {
-    const int r = 16 * tt + j;
+    const int r = min(16 * tt + j, R - 1);
 #pragma unroll
-    for (int k = 0; k < kSU; ++k) rx[tt][k] = (uint32_t)(16 * (G::kRowChunks * r + ((4 * k + q) ^ wide_swz<NT>(r))));
+    for (int k = 0; k < kSU; ++k) rx[tt][k] = (uint32_t)(16 * (G::kRowChunks * r + ((4 * k + q) ^ wide_swz<SU>(r))));
   }
 
   uint8_t* wring = smem + wave * G::template wave_bytes<kDepth>();
@@ -772,7 +785,8 @@ __global__ void __launch_bounds__(kWideWaves * 64) int4_gemm_strips_wide_kernel(
     for (int tt = 0; tt < NT; ++tt)
 #pragma unroll
       for (int v = 0; v < 4; ++v)
-        *reinterpret_cast<float2*>(sl + (16 * tt + 4 * q + v) * kStripCols + 2 * j) = float2{acc[tt][0][v], acc[tt][1][v]};
+        if (16 * tt + 4 * q + v < R)
+          *reinterpret_cast<float2*>(sl + (16 * tt + 4 * q + v) * kStripCols + 2 * j) = float2{acc[tt][0][v], acc[tt][1][v]};
 #pragma unroll
     for (int tt = 0; tt < NT; ++tt) acc[tt][0] = acc[tt][1] = float4_t{0.f, 0.f, 0.f, 0.f};
     lds_barrier();
@@ -867,16 +881,33 @@ __global__ void __launch_bounds__(kWideWaves * 64) int4_gemm_strips_wide_kernel(
 
 constexpr size_t kWideMaxLds = 156 * 1024;
 
-template <int NT>
+template <int R, int SU, int kDepth>
 static hipError_t launch_wide_one(const StripParams& P, int wgs, hipStream_t stream) {
-  const size_t lds = WideGeom<NT>::template lds_bytes<2>();
-  static_assert(WideGeom<NT>::template lds_bytes<2>() <= kWideMaxLds, "a two-stage ring must fit");
-  hipLaunchKernelGGL((int4_gemm_strips_wide_kernel<NT, 2>), dim3(wgs), dim3(kWideWaves * 64), lds, stream, P);
+  const size_t lds = WideGeom<R, SU>::template lds_bytes<kDepth>();
+  if (lds > kWideMaxLds) return hipErrorInvalidValue;  // never launch past the LDS
+  hipLaunchKernelGGL((int4_gemm_strips_wide_kernel<R, SU, kDepth>), dim3(wgs), dim3(kWideWaves * 64), lds, stream,
+                     P);
   return hipGetLastError();
 }
 
+// The deepest ring up to `depth` (2..4) that the LDS holds for SU units a
+// stage; hipErrorInvalidValue when not even two stages fit.
+template <int R, int SU>
+static hipError_t launch_wide_su(const StripParams& P, int wgs, int depth, hipStream_t stream) {
+  using G = WideGeom<R, SU>;
+  if constexpr (G::template lds_bytes<4>() <= kWideMaxLds)
+    if (depth >= 4) return launch_wide_one<R, SU, 4>(P, wgs, stream);
+  if constexpr (G::template lds_bytes<3>() <= kWideMaxLds)
+    if (depth >= 3) return launch_wide_one<R, SU, 3>(P, wgs, stream);
+  if constexpr (G::template lds_bytes<2>() <= kWideMaxLds) return launch_wide_one<R, SU, 2>(P, wgs, stream);
+  return hipErrorInvalidValue;
+}
+
+// Rows staged: N rounded up to 8, 16 or 32.  su: units a stage (0: 4 up to 8
+// rows, 2 beyond -- measured fastest; 8 rows take 2 or 4); depth: ring
+// stages (0: 2, measured fastest).
 hipError_t launch_gemm_strips_wide(const uint16_t* x, const uint8_t* w, float* y, int n, int k, int m, int wgs,
-                                   float* slots, uint32_t* status, hipStream_t stream) {
+                                   int su, int depth, float* slots, uint32_t* status, hipStream_t stream) {
   StripParams P = {};
   P.x = x; P.w = w; P.y = y; P.slots = slots; P.status = status;
   P.n = n; P.k = k; P.m = m;
@@ -885,7 +916,16 @@ hipError_t launch_gemm_strips_wide(const uint16_t* x, const uint8_t* w, float* y
   P.base = total / wgs;
   P.rem = total % wgs;
   P.y_vec = (reinterpret_cast<uintptr_t>(y) & 15) == 0 ? 1 : 0;
-  return n <= 16 ? launch_wide_one<1>(P, wgs, stream) : launch_wide_one<2>(P, wgs, stream);
+  if (depth <= 0) depth = 2;
+  if (su <= 0) su = n <= 8 ? 4 : 2;
+  if (n <= 8) return su == 2 ? launch_wide_su<8, 2>(P, wgs, depth, stream) : launch_wide_su<8, 4>(P, wgs, depth, stream);
+  if (n <= 16) {
+    if (su == 1) return launch_wide_su<16, 1>(P, wgs, depth, stream);
+    if (su == 2) return launch_wide_su<16, 2>(P, wgs, depth, stream);
+    return launch_wide_su<16, 4>(P, wgs, depth, stream);
+  }
+  if (su == 1) return launch_wide_su<32, 1>(P, wgs, depth, stream);
+  return launch_wide_su<32, 2>(P, wgs, depth, stream);
 }
 
 // ---------------------------------------------------------------------------

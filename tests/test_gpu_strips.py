@@ -127,6 +127,21 @@ def test_strip_wide_gemm_forced_plans(K, M):
         say(f"case: strip gemm K={K} M={M} N={N} as 8-row launches")
         y = batched_int4_matmul(xd, strips, K, M, strip_order=True, group=2)
         assert rel_err(y.cpu().numpy(), yref) <= TOL, (K, M, N, "slices")
+        for su, depth in ((1, 2), (1, 4), (2, 3), (4, 2)):
+            say(f"case: wide strip gemm K={K} M={M} N={N} units a stage={su} depth={depth}")
+            y = batched_int4_matmul(xd, strips, K, M, strip_order=True, group=3, front=su, batch=depth)
+            assert rel_err(y.cpu().numpy(), yref) <= TOL, (K, M, N, su, depth)
+    for N in (1, 3, 5, 8):  # 8 rows staged
+        x = O.synthetic_activations(N, K, 270 + N)
+        yref = x.astype(np.float32) @ wdq
+        xd = torch.from_numpy(x).cuda()
+        for splits in (0, 3, 100, 256):
+            for su in (0, 2):
+                if splits > total:
+                    continue
+                say(f"case: wide strip gemm K={K} M={M} N={N} workgroups={splits} units a stage={su}")
+                y = batched_int4_matmul(xd, strips, K, M, strip_order=True, group=3, splits=splits, front=su)
+                assert rel_err(y.cpu().numpy(), yref) <= TOL, (K, M, N, splits, su)
 
 
 @pytest.mark.parametrize("K,M", [(2048, 2048), (3072, 8192), (2048, 1056), (2048, 32000)])
