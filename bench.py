@@ -41,6 +41,9 @@ CONFIGS = {
     "k8192_m28672": (8192, 28672, 0.01, 1005, 0.001, [1, 32]),
     "k2048_m32000": (2048, 32000, 0.02, 1006, 0.0, [1, 2, 4, 8, 16, 32]),
     "k4096_m14336": (4096, 14336, 0.02, 1007, 0.0, [1, 2, 4, 8, 16, 32]),
+    "k2048_m6144": (2048, 6144, 0.02, 1008, 0.0, [16]),
+    "k2048_m11264": (2048, 11264, 0.02, 1009, 0.0, [16]),
+    "k5632_m2048": (5632, 2048, 0.02, 1010, 0.0, [16]),
 }
 WORKLOAD_NAMES = {
     "k2048_m2048": "int4 superblock projection 2048x2048",
@@ -49,6 +52,9 @@ WORKLOAD_NAMES = {
     "k8192_m28672": "int4 superblock projection K=8192 M=28672 (70B-class FFN, 0.1% 8-sigma outliers)",
     "k2048_m32000": "int4 superblock LM head K=2048 (hidden) x M=32000 (vocabulary), N sweep 1..32",
     "k4096_m14336": "int4 superblock FFN projection K=4096 M=14336 (8B-class), N sweep 1..32",
+    "k2048_m6144": "int4 superblock Q|K|V projection of a hidden-2048 layer (K=2048, M=3x2048)",
+    "k2048_m11264": "int4 superblock gate|up projection of a hidden-2048 layer (K=2048, M=2x5632)",
+    "k5632_m2048": "int4 superblock down projection of a hidden-2048 layer (K=5632, M=2048)",
 }
 ROTATE_BYTES = 300 * 1024 * 1024
 DEFAULT_CONFIG = "k3072_m8192"

@@ -432,8 +432,8 @@ struct StripPlan {
   int64_t workspace_bytes;
 };
 
-// Kernel choice (options `group`): 0 automatic, 1 the strip-group kernel
-// (N > 8), 2 the strip kernel (8 rows a launch), 3 the wide strip kernel.
+// Kernel choice (options `group`): 0 automatic, 1 the strip-group kernel,
+// 2 the strip kernel (8 rows a launch), 3 the wide strip kernel.
 constexpr int kStripSlices = 0, kStripGroups = 1, kStripWide = 2;
 
 bool strip_options_ok(const moat_int4_gemm_options* o) {
@@ -442,16 +442,37 @@ bool strip_options_ok(const moat_int4_gemm_options* o) {
                 (o->algo == MOAT_GEMM_AUTO || o->algo == MOAT_GEMM_MFMA || o->algo == MOAT_GEMM_DOT2));
 }
 
-// The strip kernel: workgroups, one whole strip each when M/32 is
-// 128..256 (nothing shared); otherwise up to 256 (one per CU: the kernel's
-// LDS leaves room for one), at least 16 units each.  Shared strips need the
-// status word and one slot of 8 x 32 floats per workgroup, after the fixed
-// 64 KB block.
+// The strip kernel: workgroups as strip_workgroups (at most 256, one per
+// CU: the kernel's LDS leaves room for one).  Shared strips need the status
+// word and one slot of 8 x 32 floats per workgroup, after the fixed 64 KB
+// block.
 // The wide strip kernel: all N rows in one launch, the same workgroup ranges
 // and hand-off, slots of N x 32 floats per workgroup.  The strip-group
 // kernel, over (group of 8 strips, unit) items when the records span fewer
 // than 2^32 bytes (its copy offsets are 32-bit): up to 256 workgroups of at
 // least 16 items and slots of 8 waves x 2 or 4 KB per workgroup.
+// Workgroups of the strip and wide strip kernels.  Whole strips per
+// workgroup (nothing handed between workgroups; ceil(strips / 256) strips
+// each) unless that workgroup's work exceeds the even split over 256
+// workgroups by more than 64 units, the measured cost of a hand-off: the
+// split then spreads the units over all 256 CUs, at least 16 units each.
+// (Measured: K=2048 x M=2048, 64 strips, 4.6 against 5.7 us at N = 1 as 64
+// whole strips; K=5632 x M=2048 6.5 against 9.3 us at N = 16 split over 256;
+// K=2048 x M=11264, 352 strips, 8.1 against 8.6 us as 2 strips each.)
+int strip_workgroups(int64_t strips, int64_t units, int splits) {
+  const int64_t total = strips * units;
+  int64_t wgs;
+  if (splits > 0) {
+    wgs = splits < kStripMaxWorkgroups ? splits : kStripMaxWorkgroups;
+  } else {
+    const int64_t per = (strips + kStripMaxWorkgroups - 1) / kStripMaxWorkgroups;  // strips a workgroup
+    const int64_t even = (total + kStripMaxWorkgroups - 1) / kStripMaxWorkgroups;
+    if (per * units <= even + 64) wgs = (strips + per - 1) / per;
+    else wgs = total / 16 < kStripMaxWorkgroups ? (total / 16 > 0 ? total / 16 : 1) : kStripMaxWorkgroups;
+  }
+  return (int)(wgs > total ? total : wgs);
+}
+
 StripPlan plan_strips(int32_t n, int32_t k, int32_t m, const moat_int4_gemm_options* o) {
   StripPlan p = {};
   const int64_t strips = m / 32, units = k / 32;
@@ -460,12 +481,8 @@ StripPlan plan_strips(int32_t n, int32_t k, int32_t m, const moat_int4_gemm_opti
   if (p.dot) {  // the strip kernel's VALU variant: N <= 4 only
     p.kind = kStripSlices;
     const int64_t total = strips * units;
-    int64_t wgs;
-    if (o->splits > 0) wgs = o->splits < kStripMaxWorkgroups ? o->splits : kStripMaxWorkgroups;
-    else if (strips >= 128 && strips <= 256) wgs = strips;
-    else wgs = total / 16 < 256 ? (total / 16 > 0 ? total / 16 : 1) : 256;
-    if (wgs > total) wgs = total;
-    p.wgs = (int)wgs;
+    p.wgs = strip_workgroups(strips, units, o->splits);
+    const int64_t wgs = p.wgs;
     const int waves = o->waves ? o->waves : (total / wgs <= 256 ? 12 : 8);
     p.waves = moat::strips_waves(n, waves);
     p.depth = 2;
@@ -480,14 +497,14 @@ StripPlan plan_strips(int32_t n, int32_t k, int32_t m, const moat_int4_gemm_opti
   if (forced == 3) {
     p.kind = kStripWide;
   } else if (forced == 1) {
-    if (n > kStripRowsPerLaunch && groups_fit) p.kind = kStripGroups;
+    if (groups_fit) p.kind = kStripGroups;
   } else if (forced == 0) {
     // measured: the wide kernel is the fastest for N >= 5 and, on matrices
-    // under 2^25 weights, for every N; the strip kernel (1, 2 or 4 rows
-    // staged, longer stages) for N <= 4 on larger ones; the strip-group
+    // under 2^27 weights, for every N; the strip kernel (1, 2 or 4 rows
+    // staged, 64-unit stages) for N <= 4 on larger ones; the strip-group
     // kernel (X staged once for 8 strips) for N > 16 from 2^27 weights
     if (n > 16 && weights >= ((int64_t)1 << 27) && groups_fit) p.kind = kStripGroups;
-    else if (n >= 5 || weights < ((int64_t)1 << 25)) p.kind = kStripWide;
+    else if (n >= 5 || weights < ((int64_t)1 << 27)) p.kind = kStripWide;
   }
   if (p.kind == kStripGroups) {
     const int64_t total = (strips + 7) / 8 * units;
@@ -504,12 +521,8 @@ StripPlan plan_strips(int32_t n, int32_t k, int32_t m, const moat_int4_gemm_opti
     return p;
   }
   const int64_t total = strips * units;
-  int64_t wgs;
-  if (o && o->splits > 0) wgs = o->splits < kStripMaxWorkgroups ? o->splits : kStripMaxWorkgroups;
-  else if (strips >= 128 && strips <= 256) wgs = strips;
-  else wgs = total / 16 < 256 ? (total / 16 > 0 ? total / 16 : 1) : 256;
-  if (wgs > total) wgs = total;
-  p.wgs = (int)wgs;
+  p.wgs = strip_workgroups(strips, units, o ? o->splits : 0);
+  const int64_t wgs = p.wgs;
   const int64_t base = total / wgs, rem = total % wgs;
   const bool shared = !(rem == 0 && base % units == 0);
   if (p.kind == kStripWide) {  // 8 waves; slots of n x 32 floats
