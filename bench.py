@@ -8,7 +8,8 @@ shapes; --row-order: the reference's row-order stream), fp16 activations
 ~N(0, 1), swept over N = 1, 2, 4, 8, 16, 32 parallel traces.  One "step" is
 one sweep: six projections, one per N, each on a different copy of the
 weight stream (copies rotate so that the 256 MB Infinity Cache cannot serve
-repeats: >= 300 MB of distinct records).  Beside it, the largest single-GPU
+repeats: >= 300 MB of distinct records); steps are replayed as HIP graphs of
+consecutive sweeps, as a decode loop is captured.  Beside it, the largest single-GPU
 projection, K=8192 x M=28672 (132 MB of records, 0.1 % outliers at 8 sigma),
 at N = 1, 8, 32 in strip, tile and row order.
 
@@ -235,6 +236,18 @@ class Timer:
         e1.synchronize()
         return e0.elapsed_time(e1) * 1e3
 
+    def run_us(self, graphs):
+        """Elapsed microseconds of one replay of each graph in `graphs`, in order."""
+        torch = self.torch
+        with torch.cuda.stream(self.cap):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(self.cap)
+            for g in graphs:
+                g.replay()
+            e1.record(self.cap)
+        e1.synchronize()
+        return e0.elapsed_time(e1) * 1e3
+
     def per_call_us(self, fn, calls, total_calls=200):
         g = self.capture(fn, calls)
         warm = self.replay_us([g], 1)
@@ -429,17 +442,21 @@ def main() -> int:
     per_n, call = main_res["per_n"], main_res["call"]
     copies = main_res["copies"]
 
-    # steps: one sweep over ns per step; graph s covers steps s, s+G, ... and
-    # every call of every graph reads a different weight copy
-    n_graphs = max(1, copies // len(ns))
-    step_graphs = []
-    for s_ in range(n_graphs):
-        step_graphs.append(timer.capture(lambda c, s_=s_: call(ns[c], s_ * len(ns) + c), len(ns)))
+    # steps: one sweep over ns per step, `copies` steps to a graph (a decode
+    # loop is captured whole, so one graph launch serves many steps; with
+    # one step a graph, the launch's own 2-4 us would fall on every step),
+    # call c of a graph on weight copy c % copies; exactly args.steps steps
+    # are timed (whole graphs, then one graph of the remaining steps)
+    per_graph = copies
+    full = timer.capture(lambda c: call(ns[c % len(ns)], c), per_graph * len(ns))
+    rest = args.steps % per_graph
+    tail = timer.capture(lambda c: call(ns[c % len(ns)], c), rest * len(ns)) if rest else None
     with torch.cuda.stream(timer.cap):
-        for w in range(args.warmup):
-            step_graphs[w % n_graphs].replay()
+        for _ in range(-(-args.warmup // per_graph)):
+            full.replay()
     torch.cuda.synchronize()
-    us_total = timer.replay_us(step_graphs, args.steps)
+    sequence = [full] * (args.steps // per_graph) + ([tail] if tail is not None else [])
+    us_total = timer.run_us(sequence)
     ms_step = us_total / args.steps / 1e3
     tokens = sum(ns)
     value = tokens / (ms_step / 1e3)
@@ -505,8 +522,9 @@ def main() -> int:
         "data": "synthetic",
         "config": {"workload": WORKLOAD_NAMES[args.config], "K": K, "M": M, "ns": ns,
                    "weight_copies_rotated": copies,
-                   "timing": "step: HIP graph replay of one N sweep; per N: HIP graph replay of back-to-back calls, "
-                             "HIP events on the launch stream",
+                   "timing": "steps: HIP graphs of consecutive N sweeps (one weight copy per call), exactly "
+                             "`steps` sweeps timed; per N: HIP graph replay of back-to-back calls; HIP events on the "
+                             "launch stream",
                    "algo": args.algo, "splits": args.splits, "batch": args.batch, "finish": args.finish,
                    "front": args.front, "weights": "int4 superblocks (144 B per 256 weights)"
                    + f", {layout} order",
@@ -536,7 +554,7 @@ def run_sample(args) -> int:
     the same logits."""
     import torch
     from moat_amd import _lib
-    from moat_amd.dequant import _gemm_into, quantize_to_superblocks
+    from moat_amd.dequant import _gemm_into, quantize_to_superblocks, records_to_strips
     from moat_amd.sampling import TokenSampler
 
     lib = _lib.load()
@@ -549,7 +567,7 @@ def run_sample(args) -> int:
     step = sampler.exp_lut.step_f32
     rng = np.random.default_rng(1007)
     w = torch.from_numpy(rng.standard_normal((K, V), dtype=np.float32) * np.float32(0.02)).to(dev)
-    blob0 = quantize_to_superblocks(w)
+    blob0 = records_to_strips(quantize_to_superblocks(w), K, V)  # the loader's layout for this shape
     del w
     copies = max(2, -(-ROTATE_BYTES // blob0.numel()))
     blobs = [blob0] + [blob0.clone() for _ in range(copies - 1)]
@@ -571,7 +589,7 @@ def run_sample(args) -> int:
                                           lps[N].data_ptr(), ws.data_ptr(), ws_bytes, cap.cuda_stream), "sample")
 
     def head(N, i):
-        _gemm_into(xs[N], blobs[i % copies], logits[N], K, V)
+        _gemm_into(xs[N], blobs[i % copies], logits[N], K, V, strip_order=True)
 
     with torch.cuda.stream(cap):
         for N in ns:
