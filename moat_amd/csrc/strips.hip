@@ -22,9 +22,11 @@
 //    an equal contiguous range of it (stream-K), which is one contiguous byte
 //    range of the records.  When M/32 is between 128 and 256 the plan gives
 //    every workgroup exactly one whole strip, and nothing is shared;
-//  * the W waves of a workgroup (4, 8 or 12) take every W-th unit of its
-//    range; each keeps a private LDS ring of `depth` stages of 16, 8 or 4 units
-//    (576 bytes each, copied by global_load_lds_dwordx4) with the X rows
+//  * the W waves of a workgroup (4, 8 or 12) walk its range in rounds of
+//    64, 64 or 48 consecutive units, wave w taking the w-th run of 16, 8 or 4
+//    of them (one contiguous run of records); each keeps a private LDS ring
+//    of `depth` such stages (576 bytes a unit, copied by
+//    global_load_lds_dwordx4) with the X rows
 //    those units need, issues every stage whole `depth` - 1 stages ahead, and
 //    keeps copying across strip boundaries: the ring never drains until the
 //    range ends;
@@ -74,10 +76,11 @@ struct StripParams {
 };
 
 // Geometry of a workgroup of W waves (4, 8 or 12) staging NX rows of X.
-// Wave w takes units first + W*i of its workgroup's range; one stage of a
-// wave holds 16, 8 or 4 of them (the workgroup's 64, 64 or 48 consecutive
-// units per stage round), 576 bytes each, copied by global_load_lds_dwordx4 (64 lanes x 16
-// bytes; the last copy of a stage has only as many lanes as chunks remain).
+// One stage of a wave holds 16, 8 or 4 consecutive units of its workgroup's
+// range (wave w the w-th run of the workgroup's 64, 64 or 48 consecutive
+// units per stage round), 576 bytes each, copied by global_load_lds_dwordx4
+// (64 lanes x 16 bytes; the last copy of a stage has only as many lanes as
+// chunks remain).
 // X: one copy per row of the units' 64-byte slices, rows 64 bytes apart
 // beyond their slices (a row's slices start 64 bytes further along the LDS
 // banks than the previous row's) and the 16-byte quarters of rows 4r..4r+3
@@ -268,9 +271,9 @@ __global__ void __launch_bounds__(W * 64) int4_gemm_strips_kernel(StripParams P)
   const int hi = lo + P.base + (p < P.rem ? 1 : 0);
   const MagicWords mw = magic_words();
 
-  // Weight copies: slot s = 64 i + lane of a stage carries chunk s % 36 of
-  // the stage's unit s / 36 (the stage's units lie W units apart); units
-  // past the range re-load the stage's first unit.
+  // Weight copies: a wave's stage is kSU consecutive units, one contiguous
+  // run of 576 kSU bytes; slot s = 64 i + lane carries its 16-byte chunk s
+  // (unit s / 36); units past the range re-load the stage's first unit.
   uint32_t woff[G::kWLoads], wfirst[G::kWLoads];
   int wunit[G::kWLoads];
 #pragma unroll
@@ -278,7 +281,7 @@ __global__ void __launch_bounds__(W * 64) int4_gemm_strips_kernel(StripParams P)
     const int s = min(64 * i + lane, G::kWChunks - 1);  // lanes past the last chunk copy nothing
     wunit[i] = s / 36;
     wfirst[i] = (uint32_t)(16 * (s % 36));
-    woff[i] = (uint32_t)(W * kUnitBytes * wunit[i]) + wfirst[i];
+    woff[i] = (uint32_t)(16 * s);
   }
   // X copies, one per row n (rows past N repeat row N - 1): lane l < 4 *
   // kSU carries unit l / 4, quarter (l & 3) ^ ((n >> 2) & 3).
@@ -309,9 +312,10 @@ __global__ void __launch_bounds__(W * 64) int4_gemm_strips_kernel(StripParams P)
       reinterpret_cast<uint32_t*>(smem + W * G::template wave_bytes<kDepth>() + 2 * W * G::kSlotBytes);
   status_to_lds(P.status, lds_status);  // the wave's oldest copy: the first ring wait covers it
 
-  const int first = lo + wave;  // this wave's units: first + W i
-  const int cnt = first < hi ? (hi - first + W - 1) / W : 0;
-  const int nst = (cnt + kSU - 1) / kSU;
+  // Stage s of wave w: units first + W kSU s .. + kSU - 1 (first = lo +
+  // kSU w), so that the workgroup walks W kSU consecutive units a round.
+  const int first = lo + kSU * wave;
+  const int nst = first < hi ? (hi - first + W * kSU - 1) / (W * kSU) : 0;
   // strip-relative unit of the first unit of the next stage to issue
   // (scalar, kept up to date stage by stage)
   int ub_issue = first % U;
@@ -322,13 +326,13 @@ __global__ void __launch_bounds__(W * 64) int4_gemm_strips_kernel(StripParams P)
     const uint32_t st = __builtin_amdgcn_readfirstlane(wring_lds + (s % kDepth) * G::kWStage);
 #pragma unroll
     for (int i = 0; i < G::kWLoads; ++i) {
-      const uint32_t off = u0 + W * wunit[i] < hi ? woff[i] : wfirst[i];
+      const uint32_t off = u0 + wunit[i] < hi ? woff[i] : wfirst[i];
       if (i < G::kWLoads - 1 || lane < G::kWTail) lds_dma16(base, off, st + 1024 * i);
     }
   };
   auto issue_x = [&](int s, int ub) {  // ub: strip-relative unit of the stage's first unit
-    int t = ub + W * xk;
-    if (t >= U) t -= U;  // U >= 64 > W * xk
+    int t = ub + xk;
+    if (t >= U) t -= U;  // U >= 64 > xk
     const uint32_t st = __builtin_amdgcn_readfirstlane(xring_lds + (s % kDepth) * G::kXStage);
 #pragma unroll
     for (int n = 0; n < NX; ++n)
@@ -488,13 +492,11 @@ __global__ void __launch_bounds__(W * 64) int4_gemm_strips_kernel(StripParams P)
     if (s == nst - 1) prefetch();  // no ring wait follows
     const uint8_t* wst = wring + (s % kDepth) * G::kWStage;
     const uint8_t* xst = xring + (s % kDepth) * G::kXStage;
-    const int kmax = min(kSU, cnt - kSU * s);
-    // units k < kb of this stage belong to the current part; with 64 or
-    // more units per strip, a stage (units at most 60 apart) meets at most
-    // one part boundary
-    static_assert(W * (kSU - 1) < 64, "a stage spans fewer units than a strip");
-    int kb = part_end - (first + W * kSU * s);
-    kb = kb <= 0 ? 0 : min(kmax, (kb + W - 1) / W);
+    const int u0 = first + W * kSU * s;
+    const int kmax = min(kSU, hi - u0);
+    // units k < kb of this stage belong to the current part; a stage (at
+    // most 16 consecutive units, U >= 64) meets at most one part boundary
+    const int kb = max(0, min(kmax, part_end - u0));
     // units [k_begin, k_end) of the stage: batches of 4 units, every read
     // of a batch issued before its arithmetic, where a whole batch is in
     // range; single units at the edges
@@ -625,17 +627,18 @@ hipError_t launch_gemm_strips(const uint16_t* x, const uint8_t* w, float* y, int
 }
 
 // ---------------------------------------------------------------------------
-// Wide strips: the strip kernel's walk for 9 <= N <= 32 in one launch.
-//  * the same unit ranges, stages, ring and hand-off as the strip kernel,
-//    with 8 waves and R = 8, 16 or 32 rows of X (one or two 16-row MFMA
-//    tiles on the same decoded weights; with 8 rows, lanes of tile rows 8..15
-//    read row 7 and their products are never stored), so that a strip's
-//    weights are read once for all N rows and, where the plan gives each
-//    workgroup whole strips, nothing is handed between workgroups;
-//  * a wave's stage holds SU = 1, 2 or 4 units: its X is R x SU x 64 bytes,
-//    rows kRowChunks = 4 SU
-//    16-byte chunks apart, copied as 1 KB copies that each cover 64 /
-//    kRowChunks whole rows; chunk c of row r sits at position c ^
+// Wide strips: the strip kernel's walk for up to 32 rows of X in one launch.
+//  * the same unit ranges, ring and hand-off as the strip kernel, with 8
+//    waves and R = 8, 16 or 32 rows of X (one or two 16-row MFMA tiles on the
+//    same decoded weights; with 8 rows, lanes of tile rows 8..15 read row 7
+//    and their products are never stored), so that a strip's weights are read
+//    once for all N rows and, where the plan gives each workgroup whole
+//    strips, nothing is handed between workgroups;
+//  * a wave's stage is SU = 1, 2 or 4 consecutive units (one contiguous run
+//    of 576 SU bytes of records, and 64 SU contiguous bytes of each X row);
+//    the 8 waves' stages are 8 SU consecutive units a round;
+//  * its X is R x SU x 64 bytes, rows kRowChunks = 4 SU 16-byte chunks apart,
+//    copied as 1 KB copies that each cover 64 / kRowChunks whole rows; chunk c of row r sits at position c ^
 //    wide_swz(r) of its row, so that one quarter of 16 rows falls on 16
 //    different 16-byte bank groups;
 //  * at a strip boundary every wave leaves its sums in LDS, and 2 or 4 waves
@@ -692,9 +695,9 @@ __global__ void __launch_bounds__(kWideWaves * 64) int4_gemm_strips_wide_kernel(
   const int hi = lo + P.base + (p < P.rem ? 1 : 0);
   const MagicWords mw = magic_words();
 
-  // Weight copies: slot s = 64 i + lane of a stage carries chunk s % 36 of
-  // the stage's unit s / 36 (the stage's units lie W units apart); units
-  // past the range re-load the stage's first unit.
+  // Weight copies: a wave's stage is SU consecutive units, one contiguous
+  // run of 576 SU bytes; slot s = 64 i + lane carries its 16-byte chunk s
+  // (unit s / 36); units past the range re-load the stage's first unit.
   uint32_t woff[G::kWLoads], wfirst[G::kWLoads];
   int wunit[G::kWLoads];
 #pragma unroll
@@ -702,7 +705,7 @@ __global__ void __launch_bounds__(kWideWaves * 64) int4_gemm_strips_wide_kernel(
     const int s = min(64 * i + lane, G::kWChunks - 1);  // lanes past the last chunk copy nothing
     wunit[i] = s / 36;
     wfirst[i] = (uint32_t)(16 * (s % 36));
-    woff[i] = (uint32_t)(W * kUnitBytes * wunit[i]) + wfirst[i];
+    woff[i] = (uint32_t)(16 * s);
   }
   // X copies: copy i, lane l fills position 64 i + l of the stage: row
   // r = position / kRowChunks, chunk c = (position % kRowChunks) ^
@@ -739,9 +742,10 @@ __global__ void __launch_bounds__(kWideWaves * 64) int4_gemm_strips_wide_kernel(
       reinterpret_cast<uint32_t*>(smem + W * G::template wave_bytes<kDepth>() + 2 * W * G::kSlotBytes);
   status_to_lds(P.status, lds_status);  // the wave's oldest copy: the first ring wait covers it
 
-  const int first = lo + wave;  // this wave's units: first + W i
-  const int cnt = first < hi ? (hi - first + W - 1) / W : 0;
-  const int nst = (cnt + kSU - 1) / kSU;
+  // Stage s of wave w: units first + W SU s .. + SU - 1 (first = lo + SU w),
+  // so that the workgroup walks W SU consecutive units a round.
+  const int first = lo + kSU * wave;
+  const int nst = first < hi ? (hi - first + W * kSU - 1) / (W * kSU) : 0;
   int ub_issue = first % U;  // strip-relative unit of the next stage's first unit
 
   auto issue = [&](int s) {
@@ -750,14 +754,14 @@ __global__ void __launch_bounds__(kWideWaves * 64) int4_gemm_strips_wide_kernel(
     const uint32_t wst = __builtin_amdgcn_readfirstlane(wring_lds + (s % kDepth) * G::kWStage);
 #pragma unroll
     for (int i = 0; i < G::kWLoads; ++i) {
-      const uint32_t off = u0 + W * wunit[i] < hi ? woff[i] : wfirst[i];
+      const uint32_t off = u0 + wunit[i] < hi ? woff[i] : wfirst[i];
       if (i < G::kWLoads - 1 || lane < G::kWTail) lds_dma16(base, off, wst + 1024 * i);
     }
     const uint32_t xst = __builtin_amdgcn_readfirstlane(xring_lds + (s % kDepth) * G::kXStage);
 #pragma unroll
     for (int i = 0; i < G::kXLoads; ++i) {
-      int t = ub_issue + W * xk[i];
-      if (t >= U) t -= U;  // U >= 64 > W * xk
+      int t = ub_issue + xk[i];
+      if (t >= U) t -= U;  // U >= 64 > xk
       lds_dma16(P.x, xoff[i] + 64u * (uint32_t)t, xst + 1024 * i);
     }
     ub_issue += W * kSU;
@@ -845,10 +849,11 @@ __global__ void __launch_bounds__(kWideWaves * 64) int4_gemm_strips_wide_kernel(
     else wait_vmcnt<0>();
     const uint8_t* wst = wring + (s % kDepth) * G::kWStage;
     const uint8_t* xst = xring + (s % kDepth) * G::kXStage;
-    const int kmax = min(kSU, cnt - kSU * s);
-    static_assert(W * (kSU - 1) < 64, "a stage spans fewer units than a strip");
-    int kb = part_end - (first + W * kSU * s);
-    kb = kb <= 0 ? 0 : min(kmax, (kb + W - 1) / W);
+    const int u0 = first + W * kSU * s;
+    const int kmax = min(kSU, hi - u0);
+    // units k < kb of this stage belong to the current part; a stage (SU
+    // consecutive units, U >= 64) meets at most one part boundary
+    const int kb = max(0, min(kmax, part_end - u0));
     // units [k_begin, k_end) of the stage, every read of the stage issued
     // before its arithmetic where the whole stage is in range
     auto run_units = [&](int k_begin, int k_end) {
