@@ -218,9 +218,10 @@ int32_t moat_int4_gemm_tiles(const uint16_t* x_f16, const uint8_t* tiles, float*
  * a launch; 3 the wide strip kernel), `algo` = MOAT_GEMM_DOT2 for the
  * strip kernel's vector-ALU variant (v_dot2_f32_f16 and a reduction across
  * lanes; N <= 4, MOAT_ERR_INVALID beyond), `batch` = ring depth of the strip
- * kernel (2..4) or the strip-group kernel (2 or 3), 0 automatic, `waves` =
- * waves per workgroup of the strip kernel (4, 8 or 12; 0 automatic), the
- * rest ignored.
+ * kernel or the wide strip kernel (2..4, as far as the LDS holds it) or the
+ * strip-group kernel (2 or 3), 0 automatic, `front` = units a stage of the
+ * wide strip kernel (1, 2 or 4; 0 automatic), `waves` = waves per workgroup
+ * of the strip kernel (4, 8 or 12; 0 automatic), the rest ignored.
  */
 int32_t moat_int4_records_to_strips(const uint8_t* superblocks, int32_t k, int32_t m, uint8_t* strips,
                                     hipStream_t stream);

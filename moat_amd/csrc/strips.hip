@@ -908,9 +908,10 @@ static hipError_t launch_wide_su(const StripParams& P, int wgs, int depth, hipSt
   return hipErrorInvalidValue;
 }
 
-// Rows staged: N rounded up to 8, 16 or 32.  su: units a stage (0: 4 up to 8
-// rows, 2 beyond -- measured fastest; 8 rows take 2 or 4); depth: ring
-// stages (0: 2, measured fastest).
+// Rows staged: N rounded up to 8, 16 or 32.  su: units a stage (0: 4 up to
+// 16 rows, 2 for 32 rows, whose 4-unit ring the LDS does not hold --
+// measured fastest; 8 rows take 2 or 4); depth: ring stages (0: 2, measured
+// fastest).
 hipError_t launch_gemm_strips_wide(const uint16_t* x, const uint8_t* w, float* y, int n, int k, int m, int wgs,
                                    int su, int depth, float* slots, uint32_t* status, hipStream_t stream) {
   StripParams P = {};
@@ -922,7 +923,7 @@ hipError_t launch_gemm_strips_wide(const uint16_t* x, const uint8_t* w, float* y
   P.rem = total % wgs;
   P.y_vec = (reinterpret_cast<uintptr_t>(y) & 15) == 0 ? 1 : 0;
   if (depth <= 0) depth = 2;
-  if (su <= 0) su = n <= 8 ? 4 : 2;
+  if (su <= 0) su = n <= 16 ? 4 : 2;
   if (n <= 8) return su == 2 ? launch_wide_su<8, 2>(P, wgs, depth, stream) : launch_wide_su<8, 4>(P, wgs, depth, stream);
   if (n <= 16) {
     if (su == 1) return launch_wide_su<16, 1>(P, wgs, depth, stream);
