@@ -821,7 +821,11 @@ def run_layer_driver(args) -> int:
     parts = {
         "qkv": (lambda lay: lay.attention_inputs(N), algo_bytes(N, H, qkv_m)),
         "o": (lambda lay: lay.output_projection(N), algo_bytes(N, layers[0].q_dim, H)),
-        "gate_up+swiglu": (lambda lay: lay.mlp_front(N), algo_bytes(N, H, 2 * I) + 8 * N * I + 2 * N * I),
+        # fused (strip order): weights + X + fp16 h; else the fp32 gate|up output
+        # is written, read back by the SwiGLU kernel, and h written
+        "gate_up+swiglu": (lambda lay: lay.mlp_front(N),
+                           algo_bytes(N, H, 2 * I) - 8 * N * I + 2 * N * I if layers[0].gate_up_w.fused
+                           else algo_bytes(N, H, 2 * I) + 8 * N * I + 2 * N * I),
         "down": (lambda lay: lay.down_projection(N), algo_bytes(N, I, H)),
     }
     bytes_layer = sum(b for _, b in parts.values())

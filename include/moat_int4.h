@@ -220,7 +220,7 @@ int32_t moat_int4_gemm_tiles(const uint16_t* x_f16, const uint8_t* tiles, float*
  * lanes; N <= 4, MOAT_ERR_INVALID beyond), `batch` = ring depth of the strip
  * kernel or the wide strip kernel (2..4, as far as the LDS holds it) or the
  * strip-group kernel (2 or 3), 0 automatic, `front` = units a stage of the
- * wide strip kernel (1, 2 or 4; 0 automatic), `waves` = waves per workgroup
+ * wide strip kernel (1, 2 or 4, and 8 up to 8 rows; 0 automatic), `waves` = waves per workgroup
  * of the strip kernel (4, 8 or 12; 0 automatic), the rest ignored.
  */
 int32_t moat_int4_records_to_strips(const uint8_t* superblocks, int32_t k, int32_t m, uint8_t* strips,
@@ -235,6 +235,35 @@ int64_t moat_int4_gemm_strips_workspace_size(int32_t n, int32_t k, int32_t m,
 int32_t moat_int4_gemm_strips(const uint16_t* x_f16, const uint8_t* strips, float* y_f32,
                               int32_t n, int32_t k, int32_t m, const moat_int4_gemm_options* options,
                               void* workspace, int64_t workspace_bytes, hipStream_t stream);
+
+/*
+ * The gate and up projections of a SwiGLU MLP with the activation, over
+ * strip order: h[n][m] (fp16) = fp16(silu(g) * u), g = f32(x) @
+ * f32(deq(W_gate)), u = f32(x) @ f32(deq(W_up)), silu(g) = g / (1 + exp(-g))
+ * in fp32 (moat_int4_gemm_swiglu's arithmetic, fp32 g and u).  Replaces the
+ * two dispatchGEMM calls and silu_elementwise_mul_kernel of
+ * antigravity-engine/src/transformer_engine.mm:694-713
+ * (antigravity-engine/src/shaders/transformer_ops.metal:216-232) in one
+ * launch.  `gate_up_strips`: both k x m matrices in strip order with their
+ * strips interleaved (strip 2c = strip c of W_gate, 2c + 1 = strip c of
+ * W_up), as moat_int4_interleave_strips writes it; each workgroup holds
+ * whole gate/up pairs and writes h for their 32 columns, so no workspace.
+ * Preconditions: 1 <= n <= 32, k >= 2048, k % 32 == 0, m % 32 == 0 (and 2m
+ * columns within moat_int4_gemm_strips' limits); x 16-byte aligned,
+ * gate_up_strips 16-byte aligned, h 8-byte aligned (MOAT_ERR_INVALID
+ * otherwise); options: `splits` = workgroups (0: up to 256), the rest
+ * ignored.
+ */
+int32_t moat_int4_gemm_strips_swiglu(const uint16_t* x_f16, const uint8_t* gate_up_strips, uint16_t* h_f16,
+                                     int32_t n, int32_t k, int32_t m, const moat_int4_gemm_options* options,
+                                     hipStream_t stream);
+/* Interleave two strip-order streams of k x m matrices (moat_int4_records_to_strips
+ * output): strip c of gate_strips -> strip 2c, strip c of up_strips -> strip
+ * 2c + 1 of gate_up_strips (2 x k x m x 9 / 16 bytes, not overlapping the
+ * inputs).  k % 8 == 0, m % 32 == 0.  No counterpart in the reference: the
+ * load-time layout of moat_int4_gemm_strips_swiglu's weights. */
+int32_t moat_int4_interleave_strips(const uint8_t* gate_strips, const uint8_t* up_strips, int32_t k, int32_t m,
+                                    uint8_t* gate_up_strips, hipStream_t stream);
 
 /* Zero `bytes` bytes of device memory with a kernel (no memset node). */
 int32_t moat_int4_workspace_clear(void* workspace, int64_t bytes, hipStream_t stream);

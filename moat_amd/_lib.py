@@ -57,6 +57,8 @@ SIGNATURES = {
     "moat_int4_strips_to_records": (_I32, [_P, _I32, _I32, _P, _P]),
     "moat_int4_i8_div_to_f16": (_I32, [_P, _I64, ctypes.c_float, _P, _P]),
     "moat_int4_swiglu_f32": (_I32, [_P, _I32, _I32, _I64, _P, _P]),
+    "moat_int4_gemm_strips_swiglu": (_I32, [_P, _P, _P, _I32, _I32, _I32, _P, _P]),
+    "moat_int4_interleave_strips": (_I32, [_P, _P, _I32, _I32, _P, _P]),
     "moat_int4_gemm_strips_workspace_size": (_I64, [_I32, _I32, _I32, ctypes.POINTER(GemmOptions)]),
     "moat_int4_gemm_strips": (_I32, [_P, _P, _P, _I32, _I32, _I32, ctypes.POINTER(GemmOptions), _P, _I64, _P]),
     "moat_int4_workspace_status": (_I32, [_P, _I64, ctypes.POINTER(_I32), _P]),

@@ -61,6 +61,8 @@ hipError_t launch_gemm_strips_wide(const uint16_t* x, const uint8_t* w, float* y
                                    int su, int depth, float* slots, uint32_t* status, hipStream_t stream);
 hipError_t launch_gemm_strip_groups(const uint16_t* x, const uint8_t* w, float* y, int n, int k, int m, int wgs,
                                     int depth, float* slots, uint32_t* status, hipStream_t stream);
+hipError_t launch_gemm_strips_swiglu(const uint16_t* x, const uint8_t* w, uint16_t* h, int n, int k, int m, int wgs,
+                                     int per, hipStream_t stream);
 int strip_groups_slot_bytes(int n);
 }  // namespace moat
 
@@ -438,7 +440,8 @@ constexpr int kStripSlices = 0, kStripGroups = 1, kStripWide = 2;
 
 bool strip_options_ok(const moat_int4_gemm_options* o) {
   return !o || (o->splits >= 0 && o->batch >= 0 && (o->waves == 0 || o->waves == 4 || o->waves == 8 || o->waves == 12) &&
-                o->group >= 0 && o->group <= 3 && (o->front == 0 || o->front == 1 || o->front == 2 || o->front == 4) &&
+                o->group >= 0 && o->group <= 3 &&
+                (o->front == 0 || o->front == 1 || o->front == 2 || o->front == 4 || o->front == 8) &&
                 (o->algo == MOAT_GEMM_AUTO || o->algo == MOAT_GEMM_MFMA || o->algo == MOAT_GEMM_DOT2));
 }
 
@@ -650,6 +653,43 @@ int32_t moat_int4_gemm_strips(const uint16_t* x_f16, const uint8_t* strips, floa
     if (e != hipSuccess) return MOAT_ERR_HIP;
   }
   return MOAT_OK;
+}
+
+int32_t moat_int4_interleave_strips(const uint8_t* gate_strips, const uint8_t* up_strips, int32_t k, int32_t m,
+                                    uint8_t* gate_up_strips, hipStream_t stream) {
+  if (k < 8 || (k % 8) != 0 || m < 32 || (m % 32) != 0) return MOAT_ERR_INVALID;
+  if ((int64_t)k * (m / 32) > ((int64_t)1 << 40)) return MOAT_ERR_INVALID;
+  if (!gate_strips || !up_strips || !gate_up_strips) return MOAT_ERR_INVALID;
+  const int64_t strip_bytes = (int64_t)k * 18;  // 32 columns of k rows: k / 8 records
+  const int64_t bytes = strip_bytes * (m / 32);
+  const uintptr_t o = reinterpret_cast<uintptr_t>(gate_up_strips);
+  const uintptr_t g = reinterpret_cast<uintptr_t>(gate_strips), u = reinterpret_cast<uintptr_t>(up_strips);
+  if ((g < o + (uintptr_t)(2 * bytes) && o < g + (uintptr_t)bytes) || (u < o + (uintptr_t)(2 * bytes) && o < u + (uintptr_t)bytes))
+    return MOAT_ERR_INVALID;  // the output overlaps an input
+  // strip c of gate -> strip 2c, strip c of up -> strip 2c + 1: two strided copies
+  hipError_t e = hipMemcpy2DAsync(gate_up_strips, (size_t)(2 * strip_bytes), gate_strips, (size_t)strip_bytes,
+                                  (size_t)strip_bytes, (size_t)(m / 32), hipMemcpyDeviceToDevice, stream);
+  if (e == hipSuccess)
+    e = hipMemcpy2DAsync(gate_up_strips + strip_bytes, (size_t)(2 * strip_bytes), up_strips, (size_t)strip_bytes,
+                         (size_t)strip_bytes, (size_t)(m / 32), hipMemcpyDeviceToDevice, stream);
+  return status_of(e);
+}
+
+int32_t moat_int4_gemm_strips_swiglu(const uint16_t* x_f16, const uint8_t* gate_up_strips, uint16_t* h_f16, int32_t n,
+                                     int32_t k, int32_t m, const moat_int4_gemm_options* options, hipStream_t stream) {
+  if (m < 32 || (m % 32) != 0 || m > (1 << 29) || !strips_shape_ok(n, k, 2 * m) || !strip_options_ok(options))
+    return MOAT_ERR_INVALID;
+  if (!x_f16 || !gate_up_strips || !h_f16 || !aligned(x_f16, 16) || !aligned(gate_up_strips, 16) ||
+      !aligned(h_f16, 8))
+    return MOAT_ERR_INVALID;
+  // whole gate/up pairs per workgroup (nothing is handed between workgroups)
+  const int64_t pairs = m / 32;
+  int64_t want = options && options->splits > 0 ? options->splits : kStripMaxWorkgroups;
+  if (want > kStripMaxWorkgroups) want = kStripMaxWorkgroups;
+  const int64_t per = (pairs + want - 1) / want;
+  const int64_t wgs = (pairs + per - 1) / per;
+  return status_of(
+      moat::launch_gemm_strips_swiglu(x_f16, gate_up_strips, h_f16, n, k, m, (int)wgs, (int)per, stream));
 }
 
 int32_t moat_int4_records_to_tiles(const uint8_t* superblocks, int32_t k, int32_t m, uint8_t* tiles,

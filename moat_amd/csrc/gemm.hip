@@ -128,24 +128,6 @@ __device__ __forceinline__ T select4(int i, T a0, T a1, T a2, T a3) {
   return i == 0 ? a0 : (i == 1 ? a1 : (i == 2 ? a2 : a3));
 }
 
-// SwiGLU of the two projections: silu(g) * u = g / (1 + e^-g) * u in fp32
-// (as the reference's silu_elementwise_mul_kernel), then fp16.  The empty asm
-// keeps the fp32 product a value of its own: without it the compiler fuses
-// the multiply into the fp16 conversion (v_fma_mix), one rounding where the
-// reference has two.
-__device__ __forceinline__ uint2 swiglu4(float4_t g, float4_t u) {
-  uint32_t o[2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    float a = g[2 * i] / (1.0f + expf(-g[2 * i])) * u[2 * i];
-    float b = g[2 * i + 1] / (1.0f + expf(-g[2 * i + 1])) * u[2 * i + 1];
-    asm volatile("" : "+v"(a), "+v"(b));
-    const _Float16 ha = (_Float16)a, hb = (_Float16)b;
-    o[i] = (uint32_t)__builtin_bit_cast(uint16_t, ha) | ((uint32_t)__builtin_bit_cast(uint16_t, hb) << 16);
-  }
-  return uint2{o[0], o[1]};
-}
-
 // h[r][c] = fp16(silu(g) * u), g = gu[r][c], u = gu[r][m + c] (rows ld floats
 // apart): the SwiGLU step on the output of one GEMM over gate and up stored
 // side by side, with swiglu4's arithmetic.  Four columns a thread.

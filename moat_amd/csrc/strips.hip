@@ -71,8 +71,9 @@ struct StripParams {
   uint32_t* status;    // workspace status word (null when nothing is shared)
   int n, k, m;
   int units;           // units per strip, k / 32
-  int base, rem;       // workgroup p covers units [p*base + min(p, rem), +base + (p < rem))
+  int base, rem;       // workgroup p covers units [p*base + min(p, rem), +base + (p < rem)), cut at the last unit
   int y_vec;           // y 16-byte aligned
+  uint16_t* h;         // wide kernel's SwiGLU epilogue: fp16 [n][m / 2] (else unused)
 };
 
 // Geometry of a workgroup of W waves (4, 8 or 12) staging NX rows of X.
@@ -634,29 +635,29 @@ hipError_t launch_gemm_strips(const uint16_t* x, const uint8_t* w, float* y, int
 //    and their products are never stored), so that a strip's weights are read
 //    once for all N rows and, where the plan gives each workgroup whole
 //    strips, nothing is handed between workgroups;
-//  * a wave's stage is SU = 1, 2 or 4 consecutive units (one contiguous run
-//    of 576 SU bytes of records, and 64 SU contiguous bytes of each X row);
-//    the 8 waves' stages are 8 SU consecutive units a round;
+//  * a wave's stage is SU = 1, 2, 4 or (8 rows) 8 consecutive units (one
+//    contiguous run of 576 SU bytes of records, and 64 SU contiguous bytes
+//    of each X row); the 8 waves' stages are 8 SU consecutive units a round;
 //  * its X is R x SU x 64 bytes, rows kRowChunks = 4 SU 16-byte chunks apart,
-//    copied as 1 KB copies that each cover 64 / kRowChunks whole rows; chunk c of row r sits at position c ^
-//    wide_swz(r) of its row, so that one quarter of 16 rows falls on 16
-//    different 16-byte bank groups;
+//    copied as 1 KB copies that each cover 64 / kRowChunks whole rows; chunk
+//    c of row r sits at position c ^ wide_swz(r) of its row, so that one
+//    quarter of 16 rows falls on 16 different 16-byte bank groups;
 //  * at a strip boundary every wave leaves its sums in LDS, and 2 or 4 waves
 //    each reduce and write (or hand off) 8 rows of the part.
 constexpr int kWideWaves = 8;
 
 template <int R, int SU>
 struct WideGeom {
-  static_assert(SU == 1 || SU == 2 || SU == 4, "1, 2 or 4 units a stage");
+  static_assert(SU == 1 || SU == 2 || SU == 4 || SU == 8, "1, 2, 4 or 8 units a stage");
   static_assert(R == 8 || R == 16 || R == 32, "8, 16 or 32 rows");
   static constexpr int kRows = R;                                // X rows staged (rows past N repeat row N - 1)
   static constexpr int kTiles = (R + 15) / 16;                   // 16-row MFMA tiles
   static constexpr int kStageUnits = SU;                         // a wave's units a stage
-  static constexpr int kWChunks = 36 * kStageUnits;              // 144, 72, 36
-  static constexpr int kWLoads = (kWChunks + 63) / 64;           // 3, 2, 1
-  static constexpr int kWTail = kWChunks - 64 * (kWLoads - 1);   // lanes of the last weight copy: 16, 8, 36
-  static constexpr int kWStage = 16 * kWChunks;                  // 2304, 1152, 576
-  static constexpr int kRowChunks = 4 * kStageUnits;             // 16-byte chunks of a row's stage: 16, 8, 4
+  static constexpr int kWChunks = 36 * kStageUnits;              // 288, 144, 72, 36
+  static constexpr int kWLoads = (kWChunks + 63) / 64;           // 5, 3, 2, 1
+  static constexpr int kWTail = kWChunks - 64 * (kWLoads - 1);   // lanes of the last weight copy: 32, 16, 8, 36
+  static constexpr int kWStage = 16 * kWChunks;                  // 4608, 2304, 1152, 576
+  static constexpr int kRowChunks = 4 * kStageUnits;             // 16-byte chunks of a row's stage: 32, 16, 8, 4
   static constexpr int kXStage = kRows * 16 * kRowChunks;
   static constexpr int kXLoads = kXStage / 1024;
   static_assert(kXStage % 1024 == 0, "whole 1 KB copies");
@@ -665,21 +666,28 @@ struct WideGeom {
   static constexpr int kPasses = kRows / 8;                      // output waves of a part
   template <int kDepth>
   static constexpr int wave_bytes() { return kDepth * (kWStage + kXStage); }
-  template <int kDepth>
+  static constexpr int kGateBytes = kRows * kStripCols * 4;      // SwiGLU epilogue: a gate strip's sums
+  template <int kDepth, bool kSwiglu = false>
   static constexpr size_t lds_bytes() {
-    return (size_t)kWideWaves * wave_bytes<kDepth>() + (size_t)2 * kWideWaves * kSlotBytes + kStatusLdsBytes;
+    return (size_t)kWideWaves * wave_bytes<kDepth>() + (size_t)2 * kWideWaves * kSlotBytes + kStatusLdsBytes +
+           (kSwiglu ? kGateBytes : 0);
   }
 };
 
 // Position swizzle of a row's chunks: rows r and r + 16 / kRowChunks apart
 // get different XOR patterns, so the 16 rows of a quarter spread over 16
-// bank groups (kRowChunks = 16, 8, 4: r & 15, (r >> 1) & 7, (r >> 2) & 3).
+// bank groups (kRowChunks = 32 or 16, 8, 4: r & 15, (r >> 1) & 7, (r >> 2) &
+// 3; a row of 32 chunks is two whole turns of the 16 bank groups).
 template <int SU>
 __device__ __forceinline__ int wide_swz(int r) {
-  return SU == 4 ? (r & 15) : SU == 2 ? ((r >> 1) & 7) : ((r >> 2) & 3);
+  return SU >= 4 ? (r & 15) : SU == 2 ? ((r >> 1) & 7) : ((r >> 2) & 3);
 }
 
-template <int R, int SU, int kDepth>
+// kSwiglu: the matrix is [W_gate | W_up] with their strips interleaved (strip
+// 2c gate strip c, 2c + 1 up strip c) and every workgroup holds whole pairs;
+// at a gate part the output waves keep its sums in LDS, at the up part that
+// follows they write h[r][32c + j] = fp16(silu(g) * u) instead of Y.
+template <int R, int SU, int kDepth, bool kSwiglu = false>
 __global__ void __launch_bounds__(kWideWaves * 64) int4_gemm_strips_wide_kernel(StripParams P) {
   using G = WideGeom<R, SU>;
   constexpr int NT = G::kTiles;
@@ -692,7 +700,7 @@ __global__ void __launch_bounds__(kWideWaves * 64) int4_gemm_strips_wide_kernel(
   const int p = blockIdx.x;
   const int U = P.units;
   const int lo = p * P.base + min(p, P.rem);
-  const int hi = lo + P.base + (p < P.rem ? 1 : 0);
+  const int hi = min(lo + P.base + (p < P.rem ? 1 : 0), (P.m / kStripCols) * U);
   const MagicWords mw = magic_words();
 
   // Weight copies: a wave's stage is SU consecutive units, one contiguous
@@ -740,6 +748,7 @@ __global__ void __launch_bounds__(kWideWaves * 64) int4_gemm_strips_wide_kernel(
   float* slots = reinterpret_cast<float*>(smem + W * G::template wave_bytes<kDepth>());
   uint32_t* lds_status =
       reinterpret_cast<uint32_t*>(smem + W * G::template wave_bytes<kDepth>() + 2 * W * G::kSlotBytes);
+  float* gate_lds = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(lds_status) + kStatusLdsBytes);
   status_to_lds(P.status, lds_status);  // the wave's oldest copy: the first ring wait covers it
 
   // Stage s of wave w: units first + W SU s .. + SU - 1 (first = lo + SU w),
@@ -798,12 +807,31 @@ __global__ void __launch_bounds__(kWideWaves * 64) int4_gemm_strips_wide_kernel(
     const int rp = (wave - (G::kPasses * pi) % W + W) % W;
     if (rp < G::kPasses && 8 * rp < P.n) {
       const int strip = strip0 + pi;
-      const int a = max(lo, strip * U), b = min(hi, (strip + 1) * U);
-      const bool whole = a == strip * U && b == (strip + 1) * U;
-      const bool owner = !whole && a == strip * U;
-      strip_part_out<G::kRows, W>(P, slots + (pi & 1) * W * G::kRows * kStripCols, p, strip, whole, owner,
-                                  (strip + 1) * U - 1, status_poison(status_from_lds(lds_status)), no_pre, 0,
-                                  8 * rp);
+      if constexpr (kSwiglu) {  // whole strips: the plan gives every workgroup whole gate/up pairs
+        const float* sl = slots + (pi & 1) * W * G::kRows * kStripCols;
+        const int r = 8 * rp + (lane >> 3), c4 = 4 * (lane & 7);
+        if (r < P.n) {
+          float4_t v = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int w = 0; w < W; ++w)  // in wave order
+            v += *reinterpret_cast<const float4_t*>(sl + w * G::kRows * kStripCols + r * kStripCols + c4);
+          float4_t* g = reinterpret_cast<float4_t*>(gate_lds + r * kStripCols + c4);
+          if ((strip & 1) == 0) {
+            *g = v;
+          } else {
+            const float poison = status_poison(status_from_lds(lds_status));
+            *reinterpret_cast<uint2*>(P.h + (int64_t)r * (P.m / 2) + kStripCols * (strip >> 1) + c4) =
+                swiglu4(poisoned(*g, poison), v);
+          }
+        }
+      } else {
+        const int a = max(lo, strip * U), b = min(hi, (strip + 1) * U);
+        const bool whole = a == strip * U && b == (strip + 1) * U;
+        const bool owner = !whole && a == strip * U;
+        strip_part_out<G::kRows, W>(P, slots + (pi & 1) * W * G::kRows * kStripCols, p, strip, whole, owner,
+                                    (strip + 1) * U - 1, status_poison(status_from_lds(lds_status)), no_pre, 0,
+                                    8 * rp);
+      }
     }
   };
 
@@ -886,12 +914,12 @@ __global__ void __launch_bounds__(kWideWaves * 64) int4_gemm_strips_wide_kernel(
 
 constexpr size_t kWideMaxLds = 156 * 1024;
 
-template <int R, int SU, int kDepth>
+template <int R, int SU, int kDepth, bool kSwiglu = false>
 static hipError_t launch_wide_one(const StripParams& P, int wgs, hipStream_t stream) {
-  const size_t lds = WideGeom<R, SU>::template lds_bytes<kDepth>();
+  const size_t lds = WideGeom<R, SU>::template lds_bytes<kDepth, kSwiglu>();
   if (lds > kWideMaxLds) return hipErrorInvalidValue;  // never launch past the LDS
-  hipLaunchKernelGGL((int4_gemm_strips_wide_kernel<R, SU, kDepth>), dim3(wgs), dim3(kWideWaves * 64), lds, stream,
-                     P);
+  hipLaunchKernelGGL((int4_gemm_strips_wide_kernel<R, SU, kDepth, kSwiglu>), dim3(wgs), dim3(kWideWaves * 64), lds,
+                     stream, P);
   return hipGetLastError();
 }
 
@@ -910,8 +938,8 @@ static hipError_t launch_wide_su(const StripParams& P, int wgs, int depth, hipSt
 
 // Rows staged: N rounded up to 8, 16 or 32.  su: units a stage (0: 4 up to
 // 16 rows, 2 for 32 rows, whose 4-unit ring the LDS does not hold --
-// measured fastest; 8 rows take 2 or 4); depth: ring stages (0: 2, measured
-// fastest).
+// measured fastest; 8 rows take 2, 4 or 8); depth: ring stages (0: 2,
+// measured fastest).
 hipError_t launch_gemm_strips_wide(const uint16_t* x, const uint8_t* w, float* y, int n, int k, int m, int wgs,
                                    int su, int depth, float* slots, uint32_t* status, hipStream_t stream) {
   StripParams P = {};
@@ -924,7 +952,11 @@ hipError_t launch_gemm_strips_wide(const uint16_t* x, const uint8_t* w, float* y
   P.y_vec = (reinterpret_cast<uintptr_t>(y) & 15) == 0 ? 1 : 0;
   if (depth <= 0) depth = 2;
   if (su <= 0) su = n <= 16 ? 4 : 2;
-  if (n <= 8) return su == 2 ? launch_wide_su<8, 2>(P, wgs, depth, stream) : launch_wide_su<8, 4>(P, wgs, depth, stream);
+  if (n <= 8) {
+    if (su == 2) return launch_wide_su<8, 2>(P, wgs, depth, stream);
+    if (su == 8) return launch_wide_su<8, 8>(P, wgs, depth, stream);
+    return launch_wide_su<8, 4>(P, wgs, depth, stream);
+  }
   if (n <= 16) {
     if (su == 1) return launch_wide_su<16, 1>(P, wgs, depth, stream);
     if (su == 2) return launch_wide_su<16, 2>(P, wgs, depth, stream);
@@ -932,6 +964,24 @@ hipError_t launch_gemm_strips_wide(const uint16_t* x, const uint8_t* w, float* y
   }
   if (su == 1) return launch_wide_su<32, 1>(P, wgs, depth, stream);
   return launch_wide_su<32, 2>(P, wgs, depth, stream);
+}
+
+// The wide strip kernel with its SwiGLU epilogue over the interleaved
+// [W_gate | W_up] stream of 2m columns (m gate and m up columns): wgs
+// workgroups of `per` gate/up pairs each (the last one the rest), each
+// writing h[.][32c ..) for its pairs c; rows staged and stage size as the
+// automatic plan's.
+hipError_t launch_gemm_strips_swiglu(const uint16_t* x, const uint8_t* w, uint16_t* h, int n, int k, int m, int wgs,
+                                     int per, hipStream_t stream) {
+  StripParams P = {};
+  P.x = x; P.w = w; P.h = h;
+  P.n = n; P.k = k; P.m = 2 * m;
+  P.units = k / kUnitRows;
+  P.base = 2 * per * P.units;  // whole pairs; the kernel cuts the last range at the last unit
+  P.rem = 0;
+  if (n <= 8) return launch_wide_one<8, 4, 2, true>(P, wgs, stream);
+  if (n <= 16) return launch_wide_one<16, 4, 2, true>(P, wgs, stream);
+  return launch_wide_one<32, 2, 2, true>(P, wgs, stream);
 }
 
 // ---------------------------------------------------------------------------

@@ -463,6 +463,54 @@ def int4_swiglu(x, gate_superblocks, up_superblocks, K: int, M: int):
     return res
 
 
+def interleave_strips(gate_strips, up_strips, K: int, M: int) -> torch.Tensor:
+    """The strip-order streams of two K x M matrices (:func:`records_to_strips`)
+    interleaved strip by strip: gate strip c, then up strip c.  A GPU uint8
+    tensor of both matrices' bytes, the weights of :func:`int4_swiglu_strips`.
+    (A load-time layout with no counterpart in the reference.)"""
+    K, M = int(K), int(M)
+    if K < 8 or K % 8 != 0 or M < 32 or M % 32 != 0:
+        raise ValueError(f"strip order needs K % 8 == 0 and M % 32 == 0 (got K={K}, M={M})")
+    n_sb = K * M // SUPERBLOCK_ELEMS
+    g = _blob_to_device(gate_strips, n_sb)
+    u = _blob_to_device(up_strips, n_sb)
+    out = torch.empty(2 * n_sb * SUPERBLOCK_BYTES, dtype=torch.uint8, device=g.device)
+    _lib.check(_lib.load().moat_int4_interleave_strips(D.ptr(g), D.ptr(u), K, M, D.ptr(out), D.stream()),
+               "interleave_strips")
+    return out
+
+
+def int4_swiglu_strips(x, gate_up_strips, K: int, M: int, splits: int = 0):
+    """:func:`int4_swiglu` over strip order in one launch per 32 rows of X
+    (``moat_int4_gemm_strips_swiglu``): ``gate_up_strips`` from
+    :func:`interleave_strips`; every workgroup computes whole gate/up strip
+    pairs and writes h for their 32 columns.  fp16 (N, M) out.  ValueError
+    unless ``K >= 2048``, ``K % 32 == 0`` and ``M % 32 == 0``; ``splits`` =
+    workgroups (0 automatic)."""
+    want_t = D.is_tensor(x)
+    K, M = int(K), int(M)
+    if K < 2048 or K % 32 != 0 or M < 32 or M % 32 != 0:
+        raise ValueError(f"strip order needs K >= 2048, K % 32 == 0 and M % 32 == 0 (got K={K}, M={M})")
+    xs = D.to_device(x)
+    if xs.dim() == 1:
+        xs = xs.reshape(1, -1)
+    if xs.dim() != 2 or xs.shape[1] != K:
+        raise ValueError(f"x must be (N, {K}), got {tuple(xs.shape)}")
+    if xs.dtype != torch.float16:
+        xs = xs.to(torch.float16)
+    xs = D.aligned(xs.contiguous(), 16)
+    blob = _blob_to_device(gate_up_strips, 2 * K * M // SUPERBLOCK_ELEMS)
+    N = xs.shape[0]
+    h = torch.empty((N, M), dtype=torch.float16, device=xs.device)
+    lib = _lib.load()
+    opt = _lib.GemmOptions(0, int(splits), 0, 0, 0, 0, 0)
+    for r0 in range(0, N, MAX_BATCH_PER_CALL):
+        rows = min(MAX_BATCH_PER_CALL, N - r0)
+        _lib.check(lib.moat_int4_gemm_strips_swiglu(D.ptr(xs[r0:r0 + rows]), D.ptr(blob), D.ptr(h[r0:r0 + rows]), rows,
+                                                    K, M, ctypes.byref(opt), D.stream()), "int4_swiglu_strips")
+    return h if want_t else D.to_host(h)
+
+
 def _swiglu_into(x: torch.Tensor, gate: torch.Tensor, up: torch.Tensor, h: torch.Tensor, K: int, M: int) -> None:
     """One ``moat_int4_gemm_swiglu`` launch: x (n <= 32, K) fp16 16-byte
     aligned, device record streams, (n, M) fp16 output."""

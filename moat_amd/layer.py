@@ -1,5 +1,5 @@
-"""One decoder layer's INT4 projections on MI355X, launched as four GEMMs and
-one activation kernel that a HIP graph can hold.
+"""One decoder layer's INT4 projections on MI355X, launched as four GEMMs (the
+SwiGLU activation inside the gate/up launch) that a HIP graph can hold.
 
 The projection half of ``antigravity-engine/src/transformer_engine.mm:564-730``
 (``forwardLayer``): Q, K and V from the normed hidden state (:582-591), O
@@ -16,11 +16,13 @@ Weights are stored as four matrices instead of seven: ``[W_q | W_k | W_v]``
 intermediate) and ``W_down``, each one stream of 144-byte records.  In strip
 order the stream of a column-concatenated matrix is the concatenation of
 its parts' streams (strips are column ranges, stored in column order), so
-Q/K/V are one launch and gate/up one launch; the SwiGLU kernel then reads
-gate and up from the two halves of that launch's fp32 output and writes fp16
-h, which down reads.  A matrix that strip order cannot hold (K below 2048)
-stays in row order, concatenated the same way through strip order on the
-device.
+Q/K/V are one launch.  Gate and up are one launch with the activation: their
+strips interleaved (gate strip c, then up strip c), every workgroup holding
+whole gate/up pairs and writing fp16 h = silu(gate) * up for their columns
+(``moat_int4_gemm_strips_swiglu``), which down reads.  A matrix that strip
+order cannot hold (K below 2048) stays in row order, concatenated the same
+way through strip order on the device; there gate|up is one launch with an
+fp32 output and the SwiGLU kernel makes h from its two halves.
 
 All buffers (inputs, outputs, one GEMM workspace) are allocated once, for
 ``max_batch`` rows, so that every launch of a call with ``n <= max_batch``
@@ -103,6 +105,43 @@ class _Matrix:
                           ctypes.byref(opt), ws.data_ptr(), ws.numel(), D.stream()), what)
 
 
+class _GateUp:
+    """Gate and up with the activation: in strip order their strips
+    interleaved for one ``moat_int4_gemm_strips_swiglu`` launch that writes
+    h; otherwise ``[W_gate | W_up]`` (fp32 out) and the SwiGLU kernel."""
+
+    def __init__(self, gate, up, K: int, inter: int) -> None:
+        self.K, self.inter = K, inter
+        self.fused = strip_layout_ok((K, 2 * inter)) and inter % 32 == 0
+        if self.fused:
+            g, u = _strips_of(gate), _strips_of(up)
+            self.blob = torch.empty(2 * g.numel(), dtype=torch.uint8, device=g.device)
+            _lib.check(_lib.load().moat_int4_interleave_strips(g.data_ptr(), u.data_ptr(), K, inter,
+                                                               self.blob.data_ptr(), D.stream()),
+                       "moat_int4_interleave_strips")
+            self.strip = True
+        else:
+            self.mat = _Matrix([gate, up], K, 2 * inter)
+            self.blob, self.strip = self.mat.blob, self.mat.strip
+
+    def workspace_bytes(self, n: int) -> int:
+        return 0 if self.fused else self.mat.workspace_bytes(n)
+
+    def launch(self, x: torch.Tensor, gate_up, h: torch.Tensor, n: int, ws: torch.Tensor, what: str) -> None:
+        lib = _lib.load()
+        if self.fused:
+            opt = _lib.GemmOptions()
+            for r0 in range(0, n, MAX_BATCH_PER_CALL):
+                rows = min(MAX_BATCH_PER_CALL, n - r0)
+                _lib.check(lib.moat_int4_gemm_strips_swiglu(x[r0].data_ptr(), self.blob.data_ptr(), h[r0].data_ptr(),
+                                                            rows, self.K, self.inter, ctypes.byref(opt), D.stream()),
+                           what)
+            return
+        self.mat.launch(x, gate_up, n, ws, what)
+        _lib.check(lib.moat_int4_swiglu_f32(gate_up.data_ptr(), n, self.inter, 2 * self.inter, h.data_ptr(),
+                                            D.stream()), what + " (swiglu)")
+
+
 class LayerProjections:
     """The seven projections of one decoder layer, held on the GPU.
 
@@ -119,8 +158,9 @@ class LayerProjections:
     inputs ``x`` (hidden state, fp16), ``attn`` (attention output, fp16),
     ``x_mlp`` (post-attention normed state, fp16); outputs ``qkv`` (fp32, Q
     then K then V per row, also as the views ``q``, ``k``, ``v``), ``o``
-    (fp32), ``gate_up`` (fp32, gate then up per row), ``h`` (fp16
-    ``silu(gate) * up``) and ``down`` (fp32)."""
+    (fp32), ``h`` (fp16 ``silu(gate) * up``), ``down`` (fp32), and, where
+    gate and up are not fused with the activation (row order), ``gate_up``
+    (fp32, gate then up per row; else None)."""
 
     def __init__(self, weights: Mapping[str, Any], max_batch: int = 32) -> None:
         missing = [n for n in NAMES if n not in weights]
@@ -144,7 +184,7 @@ class LayerProjections:
         self.max_batch = int(max_batch)
         self.qkv_w = _Matrix([weights["q_proj"], weights["k_proj"], weights["v_proj"]], H, q_dim + 2 * kv_dim)
         self.o_w = _Matrix([weights["o_proj"]], q_dim, H)
-        self.gate_up_w = _Matrix([weights["gate_proj"], weights["up_proj"]], H, 2 * inter)
+        self.gate_up_w = _GateUp(weights["gate_proj"], weights["up_proj"], H, inter)
         self.down_w = _Matrix([weights["down_proj"]], inter, H)
         mats = (self.qkv_w, self.o_w, self.gate_up_w, self.down_w)
         ws_bytes = max(m.workspace_bytes(n) for m in mats for n in range(1, min(self.max_batch, MAX_BATCH_PER_CALL) + 1))
@@ -162,7 +202,7 @@ class LayerProjections:
         self.k = self.qkv[:, q_dim:q_dim + kv_dim]
         self.v = self.qkv[:, q_dim + kv_dim:]
         self.o = torch.empty((B, H), dtype=f32, device=dev)
-        self.gate_up = torch.empty((B, 2 * inter), dtype=f32, device=dev)
+        self.gate_up = None if self.gate_up_w.fused else torch.empty((B, 2 * inter), dtype=f32, device=dev)
         self.h = torch.empty((B, inter), dtype=f16, device=dev)
         self.down = torch.empty((B, H), dtype=f32, device=dev)
         self._graphs: Dict[int, torch.cuda.CUDAGraph] = {}
@@ -193,13 +233,10 @@ class LayerProjections:
         self.o_w.launch(self.attn, self.o, n, self.workspace, "LayerProjections.o")
 
     def mlp_front(self, n: int) -> None:
-        """Enqueue gate|up = x_mlp[:n] @ [W_gate | W_up] (one launch) and h =
-        fp16(silu(gate) * up)."""
+        """Enqueue h = fp16(silu(x_mlp[:n] @ W_gate) * (x_mlp[:n] @ W_up)): one
+        launch in strip order, else the gate|up launch and the SwiGLU kernel."""
         n = self._rows(n)
-        self.gate_up_w.launch(self.x_mlp, self.gate_up, n, self.workspace, "LayerProjections.gate_up")
-        I = self.intermediate
-        _lib.check(_lib.load().moat_int4_swiglu_f32(self.gate_up.data_ptr(), n, I, 2 * I, self.h.data_ptr(),
-                                                    D.stream()), "LayerProjections.swiglu")
+        self.gate_up_w.launch(self.x_mlp, self.gate_up, self.h, n, self.workspace, "LayerProjections.gate_up")
 
     def down_projection(self, n: int) -> None:
         """Enqueue down = h[:n] @ W_down."""

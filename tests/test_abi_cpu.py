@@ -293,6 +293,46 @@ def test_tile_order_entry_points_validate(lib):
     assert lib.moat_int4_gemm_tiles(FAKE, FAKE, big, 33, 2048, 2048, ctypes.byref(opt), big, 1 << 30, None) == I
 
 
+def test_strip_swiglu_entry_points_validate(lib):
+    I = _lib.MOAT_ERR_INVALID
+    opt = _lib.GemmOptions(0, 0, 0, 0, 0, 0, 0)
+    big = ctypes.c_void_p(0x90000000)
+    # moat_int4_gemm_strips_swiglu(x, gate_up_strips, h, n, k, m, options, stream)
+    f = lib.moat_int4_gemm_strips_swiglu
+    assert f(FAKE, FAKE, big, 0, 2048, 5632, ctypes.byref(opt), None) == I     # n < 1
+    assert f(FAKE, FAKE, big, 33, 2048, 5632, ctypes.byref(opt), None) == I    # n > 32
+    assert f(FAKE, FAKE, big, 1, 2016, 5632, ctypes.byref(opt), None) == I     # k < 2048
+    assert f(FAKE, FAKE, big, 1, 2056, 5632, ctypes.byref(opt), None) == I     # k % 32
+    assert f(FAKE, FAKE, big, 1, 2048, 5616, ctypes.byref(opt), None) == I     # m % 32
+    assert f(FAKE, FAKE, big, 1, 2048, 0, ctypes.byref(opt), None) == I
+    assert f(FAKE, FAKE, big, 1, 2048, 1 << 30, ctypes.byref(opt), None) == I  # 2m columns too many
+    assert f(ctypes.c_void_p(0x10008), FAKE, big, 1, 2048, 5632, ctypes.byref(opt), None) == I  # x 16 B
+    assert f(FAKE, ctypes.c_void_p(0x10008), big, 1, 2048, 5632, ctypes.byref(opt), None) == I  # strips 16 B
+    assert f(FAKE, FAKE, ctypes.c_void_p(0x90000004), 1, 2048, 5632, ctypes.byref(opt), None) == I  # h 8 B
+    assert f(None, FAKE, big, 1, 2048, 5632, ctypes.byref(opt), None) == I
+    assert f(FAKE, None, big, 1, 2048, 5632, ctypes.byref(opt), None) == I
+    assert f(FAKE, FAKE, None, 1, 2048, 5632, ctypes.byref(opt), None) == I
+    bad = _lib.GemmOptions(0, -1, 0, 0, 0, 0, 0)
+    assert f(FAKE, FAKE, big, 1, 2048, 5632, ctypes.byref(bad), None) == I     # negative splits
+    # moat_int4_interleave_strips(gate, up, k, m, out, stream)
+    g = lib.moat_int4_interleave_strips
+    assert g(FAKE, ctypes.c_void_p(0x20000000), 2044, 64, big, None) == I      # k % 8
+    assert g(FAKE, ctypes.c_void_p(0x20000000), 2048, 48, big, None) == I      # m % 32
+    assert g(None, ctypes.c_void_p(0x20000000), 2048, 64, big, None) == I
+    assert g(FAKE, ctypes.c_void_p(0x20000000), 2048, 64, None, None) == I
+    assert g(FAKE, ctypes.c_void_p(0x20000000), 2048, 64, FAKE, None) == I     # output overlaps gate
+    assert g(FAKE, ctypes.c_void_p(0x20000000), 2048, 64, ctypes.c_void_p(0x20000000 - 4096), None) == I  # and up
+
+
+def test_strip_swiglu_python_checks_first():
+    import numpy as np
+    from moat_amd import dequant
+    with pytest.raises(ValueError):
+        dequant.int4_swiglu_strips(np.zeros((1, 1024), np.float16), None, 1024, 64)
+    with pytest.raises(ValueError):
+        dequant.interleave_strips(None, None, 2048, 40)
+
+
 def test_tile_order_python_checks_first():
     import numpy as np
     from moat_amd import dequant

@@ -136,7 +136,7 @@ def test_strip_wide_gemm_forced_plans(K, M):
         yref = x.astype(np.float32) @ wdq
         xd = torch.from_numpy(x).cuda()
         for splits in (0, 3, 100, 256):
-            for su in (0, 2):
+            for su in (0, 2, 8):
                 if splits > total:
                     continue
                 say(f"case: wide strip gemm K={K} M={M} N={N} workgroups={splits} units a stage={su}")
