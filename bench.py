@@ -476,6 +476,17 @@ def main() -> int:
         side = {"workload": WORKLOAD_NAMES[side_cfg], "K": CONFIGS[side_cfg][0], "M": CONFIGS[side_cfg][1],
                 "ns": side_ns, **side}
 
+    layer_driver = None
+    if args.config == DEFAULT_CONFIG and not args.no_side and not args.ns:
+        torch.cuda.empty_cache()
+        d = measure_layer_driver(args, with_cpu=False)
+        layer_driver = {"workload": d["config"]["workload"], "n": d["config"]["n"],
+                        "us_per_layer": round(d["ms_per_step"] * 1e3, 3), "tok_s": d["value"],
+                        "layers_in_graph": d["config"]["layers_in_graph"], "layouts": d["config"]["layouts"],
+                        "per_launch": d["per_launch"], "roofline": d["roofline"]}
+        del d
+        torch.cuda.empty_cache()
+
     dom = max(ns, key=lambda n: per_n[n]["us_per_call"])
     roof = {
         "bound": "hbm",
@@ -532,6 +543,7 @@ def main() -> int:
         "per_n": {str(k): v for k, v in per_n.items()},
         "read_floor": main_res["read_floor"],
         "largest_projection": side,
+        "layer_driver": layer_driver,
         "roofline": roof,
         "cpu_baseline": cpu,
     }
@@ -753,13 +765,13 @@ def run_quantize_load(args) -> int:
     return 0
 
 
-def run_layer_driver(args) -> int:
+def measure_layer_driver(args, with_cpu: bool = True) -> dict:
     """One decoder layer's projections through moat_amd.layer.LayerProjections
-    at N = 16: Q|K|V in one strip-order launch, O, gate|up in one launch, the
-    SwiGLU kernel (fp16 h) and down(h), captured in one HIP graph that holds
-    `copies` distinct layers (>= 300 MB of records, so no layer is served from
-    the Infinity Cache), like consecutive layers of a model.  A step is one
-    layer."""
+    at N = 16: Q|K|V in one strip-order launch, O, gate|up with the SwiGLU
+    epilogue in one launch (fp16 h) and down(h), captured in one HIP graph that
+    holds `copies` distinct layers (>= 300 MB of records, so no layer is served
+    from the Infinity Cache), like consecutive layers of a model.  A step is
+    one layer.  Returns the JSON object of the measurement."""
     import torch
     from moat_amd.dequant import quantize_to_superblocks
     from moat_amd.layer import LayerProjections
@@ -844,7 +856,7 @@ def run_layer_driver(args) -> int:
         lay.check()
 
     cpu = None
-    if not args.no_cpu_baseline:
+    if with_cpu and not args.no_cpu_baseline:
         sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
         from oracle import superblock_oracle as O
         hosts = {k: r.cpu().numpy() for k, (r, K, M) in first.items()}
@@ -872,8 +884,8 @@ def run_layer_driver(args) -> int:
         "ms_per_step": round(us / 1e3, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f16", "data": "synthetic",
         "config": {"workload": "decoder layer projections at hidden 2048 (Q,K,V,O 2048x2048, gate/up 2048x5632, "
-                               f"down 5632x2048), N={N}, through the layer driver: Q|K|V one launch, O, gate|up one "
-                               "launch + SwiGLU to fp16 h, down(h), one graph over consecutive layers",
+                               f"down 5632x2048), N={N}, through the layer driver: Q|K|V one launch, O, gate|up "
+                               "with SwiGLU one launch (fp16 h), down(h), one graph over consecutive layers",
                    "n": N, "layouts": layers[0].layouts, "layers_in_graph": copies,
                    "timing": "HIP graph replay, HIP events on the launch stream",
                    "weights": "int4 superblocks (144 B per 256 weights)", "activations": "fp16", "output": "fp32"},
@@ -883,7 +895,11 @@ def run_layer_driver(args) -> int:
                      "kernel": f"layer: {bytes_layer} algorithmic B per layer / {us:.2f} us per layer"},
         "cpu_baseline": cpu,
     }
-    print(json.dumps(out), flush=True)
+    return out
+
+
+def run_layer_driver(args) -> int:
+    print(json.dumps(measure_layer_driver(args)), flush=True)
     return 0
 
 
