@@ -287,12 +287,13 @@ __global__ void __launch_bounds__(W * 64) int4_gemm_strips_kernel(StripParams P)
   // X copies, one per row n (rows past N repeat row N - 1): lane l < 4 *
   // kSU carries unit l / 4, quarter (l & 3) ^ ((n >> 2) & 3).
   const int xk = lane >> 2;
-  uint32_t xoff[NX];
+  uint32_t xoff[NX], xflat[NX];
 #pragma unroll
   for (int n = 0; n < NX; ++n) {
     const int row = min(n, P.n - 1);
     const int quarter = (lane & 3) ^ ((n >> 2) & 3);
     xoff[n] = (uint32_t)(2 * (row * P.k + 8 * quarter));
+    xflat[n] = xoff[n] + 64u * (uint32_t)xk;  // from the stage's first unit when no unit wraps
   }
   // LDS reads of a unit k: record q's 8 row scales, the 8 bytes of column
   // pair j of its rows, and X row j's quarter q (rows past N read row N - 1,
@@ -321,23 +322,40 @@ __global__ void __launch_bounds__(W * 64) int4_gemm_strips_kernel(StripParams P)
   // (scalar, kept up to date stage by stage)
   int ub_issue = first % U;
 
+  // A stage's copies take per-lane offsets fixed for the whole call (a
+  // scalar base moves) unless the stage runs past the range (its weights) or
+  // a unit wraps into the next strip (its X): those stages, uniform
+  // branches, select per lane.
   auto issue_w = [&](int s) {
     const int u0 = first + W * kSU * s;
     const uint8_t* base = P.w + (uint64_t)u0 * kUnitBytes;
     const uint32_t st = __builtin_amdgcn_readfirstlane(wring_lds + (s % kDepth) * G::kWStage);
+    if (u0 + kSU <= hi) {
 #pragma unroll
-    for (int i = 0; i < G::kWLoads; ++i) {
-      const uint32_t off = u0 + wunit[i] < hi ? woff[i] : wfirst[i];
-      if (i < G::kWLoads - 1 || lane < G::kWTail) lds_dma16(base, off, st + 1024 * i);
+      for (int i = 0; i < G::kWLoads; ++i)
+        if (i < G::kWLoads - 1 || lane < G::kWTail) lds_dma16(base, woff[i], st + 1024 * i);
+    } else {
+#pragma unroll
+      for (int i = 0; i < G::kWLoads; ++i) {
+        const uint32_t off = u0 + wunit[i] < hi ? woff[i] : wfirst[i];
+        if (i < G::kWLoads - 1 || lane < G::kWTail) lds_dma16(base, off, st + 1024 * i);
+      }
     }
   };
   auto issue_x = [&](int s, int ub) {  // ub: strip-relative unit of the stage's first unit
-    int t = ub + xk;
-    if (t >= U) t -= U;  // U >= 64 > xk
     const uint32_t st = __builtin_amdgcn_readfirstlane(xring_lds + (s % kDepth) * G::kXStage);
+    if (ub + kSU <= U) {
+      const uint8_t* xb = reinterpret_cast<const uint8_t*>(P.x) + 64 * ub;
 #pragma unroll
-    for (int n = 0; n < NX; ++n)
-      if (lane < G::kXLanes) lds_dma16(P.x, xoff[n] + 64u * (uint32_t)t, st + G::kXRowBytes * n);
+      for (int n = 0; n < NX; ++n)
+        if (lane < G::kXLanes) lds_dma16(xb, xflat[n], st + G::kXRowBytes * n);
+    } else {
+      int t = ub + xk;
+      if (t >= U) t -= U;  // U >= 64 > xk
+#pragma unroll
+      for (int n = 0; n < NX; ++n)
+        if (lane < G::kXLanes) lds_dma16(P.x, xoff[n] + 64u * (uint32_t)t, st + G::kXRowBytes * n);
+    }
   };
 
   // Stages go out whole (weights, then X), kDepth - 1 ahead of the one in
@@ -719,7 +737,7 @@ __global__ void __launch_bounds__(kWideWaves * 64) int4_gemm_strips_wide_kernel(
   // r = position / kRowChunks, chunk c = (position % kRowChunks) ^
   // wide_swz(r), i.e. quarter c % 4 of the stage's unit c / 4 (rows past N
   // read row N - 1)
-  uint32_t xoff[G::kXLoads];
+  uint32_t xoff[G::kXLoads], xflat[G::kXLoads];
   int xk[G::kXLoads];
 #pragma unroll
   for (int i = 0; i < G::kXLoads; ++i) {
@@ -728,6 +746,7 @@ __global__ void __launch_bounds__(kWideWaves * 64) int4_gemm_strips_wide_kernel(
     const int c = (pos % G::kRowChunks) ^ wide_swz<SU>(r);
     xk[i] = c >> 2;
     xoff[i] = (uint32_t)(2 * (min(r, P.n - 1) * P.k + 8 * (c & 3)));
+    xflat[i] = xoff[i] + 64u * (uint32_t)xk[i];  // from the stage's first unit when no unit wraps
   }
   // LDS reads of unit k of a stage: record q's 8 row scales, the 8 bytes of
   // column pair j, and quarter q of X row 16 tt + j (past the staged rows:
@@ -757,21 +776,37 @@ __global__ void __launch_bounds__(kWideWaves * 64) int4_gemm_strips_wide_kernel(
   const int nst = first < hi ? (hi - first + W * kSU - 1) / (W * kSU) : 0;
   int ub_issue = first % U;  // strip-relative unit of the next stage's first unit
 
+  // A stage's copies take per-lane offsets fixed for the whole call (a
+  // scalar base moves) unless the stage runs past the range (its weights) or
+  // a unit wraps into the next strip (its X): those stages, uniform
+  // branches, select per lane.
   auto issue = [&](int s) {
     const int u0 = first + W * kSU * s;
     const uint8_t* base = P.w + (uint64_t)u0 * kUnitBytes;
     const uint32_t wst = __builtin_amdgcn_readfirstlane(wring_lds + (s % kDepth) * G::kWStage);
+    if (u0 + kSU <= hi) {
 #pragma unroll
-    for (int i = 0; i < G::kWLoads; ++i) {
-      const uint32_t off = u0 + wunit[i] < hi ? woff[i] : wfirst[i];
-      if (i < G::kWLoads - 1 || lane < G::kWTail) lds_dma16(base, off, wst + 1024 * i);
+      for (int i = 0; i < G::kWLoads; ++i)
+        if (i < G::kWLoads - 1 || lane < G::kWTail) lds_dma16(base, woff[i], wst + 1024 * i);
+    } else {
+#pragma unroll
+      for (int i = 0; i < G::kWLoads; ++i) {
+        const uint32_t off = u0 + wunit[i] < hi ? woff[i] : wfirst[i];
+        if (i < G::kWLoads - 1 || lane < G::kWTail) lds_dma16(base, off, wst + 1024 * i);
+      }
     }
     const uint32_t xst = __builtin_amdgcn_readfirstlane(xring_lds + (s % kDepth) * G::kXStage);
+    if (ub_issue + kSU <= U) {
+      const uint8_t* xb = reinterpret_cast<const uint8_t*>(P.x) + 64 * ub_issue;
 #pragma unroll
-    for (int i = 0; i < G::kXLoads; ++i) {
-      int t = ub_issue + xk[i];
-      if (t >= U) t -= U;  // U >= 64 > xk
-      lds_dma16(P.x, xoff[i] + 64u * (uint32_t)t, xst + 1024 * i);
+      for (int i = 0; i < G::kXLoads; ++i) lds_dma16(xb, xflat[i], xst + 1024 * i);
+    } else {
+#pragma unroll
+      for (int i = 0; i < G::kXLoads; ++i) {
+        int t = ub_issue + xk[i];
+        if (t >= U) t -= U;  // U >= 64 > xk
+        lds_dma16(P.x, xoff[i] + 64u * (uint32_t)t, xst + 1024 * i);
+      }
     }
     ub_issue += W * kSU;
     while (ub_issue >= U) ub_issue -= U;
