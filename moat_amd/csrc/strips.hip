@@ -500,14 +500,40 @@ __global__ void __launch_bounds__(W * 64) int4_gemm_strips_kernel(StripParams P)
   };
 
   constexpr int kLS = G::kWLoads + NX;  // copies per stage
-  for (int s = 0; s < nst; ++s) {
+  // Issue the stage kDepth - 1 ahead, then wait for stage s (the later
+  // stages stay in flight).
+  auto next_stage = [&](int s) {
     if (s + kDepth - 1 < nst) issue(s + kDepth - 1);
-    // stages issued after this one
-    const int ahead = min(kDepth - 1, nst - 1 - s);
+    const int ahead = min(kDepth - 1, nst - 1 - s);  // stages issued after this one
     if (ahead >= 3) wait_vmcnt<3 * kLS>();
     else if (ahead == 2) wait_vmcnt<2 * kLS>();
     else if (ahead == 1) wait_vmcnt<kLS>();
     else wait_vmcnt<0>();
+  };
+  int s = 0;
+  while (s < nst) {
+    // Stages whose units all lie in range and in the current part (u0 + kSU
+    // <= part_end <= hi), the last one aside, run in a loop of one path:
+    // batches of 4 units, every read of a batch before its arithmetic, the
+    // accumulators carried in the same registers from stage to stage.
+    const int room = part_end - kSU - first;
+    const int s_clean = room < 0 ? s : min(nst - 1, max(s, room / (W * kSU) + 1));
+    for (; s < s_clean; ++s) {
+      next_stage(s);
+      const uint8_t* wst = wring + (s % kDepth) * G::kWStage;
+      const uint8_t* xst = xring + (s % kDepth) * G::kXStage;
+#pragma unroll
+      for (int k0 = 0; k0 < kSU; k0 += 4) {
+        UnitRegs r[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) load_unit(r[u], wst + kUnitBytes * (k0 + u), xst + 64 * (k0 + u));
+#pragma unroll
+        for (int u = 0; u < 4; ++u) math_unit(r[u]);
+      }
+    }
+    if (s >= nst) break;
+    // a stage that meets the part's end or the range's end, or the last one
+    next_stage(s);
     if (s == nst - 1) prefetch();  // no ring wait follows
     const uint8_t* wst = wring + (s % kDepth) * G::kWStage;
     const uint8_t* xst = xring + (s % kDepth) * G::kXStage;
@@ -543,6 +569,7 @@ __global__ void __launch_bounds__(W * 64) int4_gemm_strips_kernel(StripParams P)
       part_end = min(hi, part_end + U);
       run_units(kb, kmax);
     }
+    ++s;
   }
   // the parts this wave has not flushed yet (always the last; also any it
   // holds no unit of)
@@ -903,13 +930,37 @@ __global__ void __launch_bounds__(kWideWaves * 64) int4_gemm_strips_wide_kernel(
     }
   };
 
-  for (int s = 0; s < nst; ++s) {
+  // Issue the stage kDepth - 1 ahead, then wait for stage s (the later
+  // stages stay in flight).
+  auto next_stage = [&](int s) {
     if (s + kDepth - 1 < nst) issue(s + kDepth - 1);
     const int ahead = min(kDepth - 1, nst - 1 - s);  // stages issued after this one
     if (ahead >= 3) wait_vmcnt<3 * G::kLS>();
     else if (ahead == 2) wait_vmcnt<2 * G::kLS>();
     else if (ahead == 1) wait_vmcnt<G::kLS>();
     else wait_vmcnt<0>();
+  };
+  int s = 0;
+  while (s < nst) {
+    // Stages whose units all lie in range and in the current part (u0 + SU
+    // <= part_end <= hi) run in a loop of one path: every read of the stage,
+    // then its arithmetic, the accumulators carried in the same registers
+    // from stage to stage.
+    const int room = part_end - kSU - first;
+    const int s_clean = room < 0 ? s : min(nst, max(s, room / (W * kSU) + 1));
+    for (; s < s_clean; ++s) {
+      next_stage(s);
+      const uint8_t* wst = wring + (s % kDepth) * G::kWStage;
+      const uint8_t* xst = xring + (s % kDepth) * G::kXStage;
+      UnitRegs r[kSU];
+#pragma unroll
+      for (int k = 0; k < kSU; ++k) load_unit(r[k], wst, xst, k);
+#pragma unroll
+      for (int k = 0; k < kSU; ++k) math_unit(r[k]);
+    }
+    if (s >= nst) break;
+    // a stage that meets the part's end or the range's end
+    next_stage(s);
     const uint8_t* wst = wring + (s % kDepth) * G::kWStage;
     const uint8_t* xst = xring + (s % kDepth) * G::kXStage;
     const int u0 = first + W * kSU * s;
@@ -943,6 +994,7 @@ __global__ void __launch_bounds__(kWideWaves * 64) int4_gemm_strips_wide_kernel(
       part_end = min(hi, part_end + U);
       run_units(kb, kmax);
     }
+    ++s;
   }
   for (; part < nparts; ++part) flush(part);
 }
