@@ -1194,7 +1194,9 @@ __global__ void __launch_bounds__(kGroupWaves * 64) int4_gemm_strip_groups_kerne
   const int nst = (hi - lo + kSU - 1) / kSU;  // the same for every wave
   // group and strip-relative unit of the next stage to issue (scalars)
   int g_issue = lo / U, u_issue = lo - g_issue * U;
-  auto issue = [&](int s) {
+  // A stage's copies: the wave's own weights (its private ring) and its
+  // share of the workgroup's X stage; g_issue / u_issue advance after the X.
+  auto issue_w = [&](int s) {
     const int t0 = lo + kSU * s;
     const uint32_t wst = __builtin_amdgcn_readfirstlane(wring_lds + (s % kDepth) * kGroupWStage);
 #pragma unroll
@@ -1206,6 +1208,9 @@ __global__ void __launch_bounds__(kGroupWaves * 64) int4_gemm_strip_groups_kerne
       const uint32_t off = (uint32_t)(strip * U + u) * (uint32_t)kUnitBytes + wchunk[i];
       if (i < kGroupWLoads - 1 || lane < kGroupWTail) lds_dma16(P.w, off, wst + 1024 * i);
     }
+  };
+  auto issue_x = [&](int s) {
+    const int t0 = lo + kSU * s;
     int ux = u_issue + xk;
     if (ux >= U) ux -= U;
     if (t0 + xk >= hi) ux = u_issue;
@@ -1213,6 +1218,10 @@ __global__ void __launch_bounds__(kGroupWaves * 64) int4_gemm_strip_groups_kerne
               __builtin_amdgcn_readfirstlane(xring_lds + (s % kDepth) * G::kXStage + 1024 * xc));
     u_issue += kSU;
     if (u_issue >= U) { u_issue -= U; ++g_issue; }
+  };
+  auto issue = [&](int s) {
+    issue_w(s);
+    issue_x(s);
   };
 #pragma unroll
   for (int s = 0; s < kDepth - 1; ++s)
@@ -1375,15 +1384,28 @@ __global__ void __launch_bounds__(kGroupWaves * 64) int4_gemm_strip_groups_kerne
   };
 
   for (int s = 0; s < nst; ++s) {
-    // stages issued after this one (all waves alike)
-    const int ahead = min(kDepth - 2, nst - 1 - s);
-    if (ahead >= 2) wait_vmcnt<2 * (kGroupWLoads + 1)>();
-    else if (ahead == 1) wait_vmcnt<kGroupWLoads + 1>();
-    else wait_vmcnt<0>();
-    // every wave's copies of stage s have landed, and every wave is done
-    // with stage s - 1, whose buffers the next issue refills
-    lds_barrier();
-    if (s + kDepth - 1 < nst) issue(s + kDepth - 1);
+    if constexpr (kDepth == 2) {
+      // the wave's own weights for stage s + 1 go out before the wait (its
+      // ring slot held stage s - 1, which this wave has finished), the X
+      // share after the barrier (every wave has finished reading stage
+      // s - 1's X): the weights stay two stages ahead
+      const bool more = s + 1 < nst;
+      if (more) issue_w(s + 1);
+      if (more) wait_vmcnt<kGroupWLoads>();  // stage s landed; W(s + 1) in flight
+      else wait_vmcnt<0>();
+      lds_barrier();  // every wave's copies of stage s have landed
+      if (more) issue_x(s + 1);
+    } else {
+      // stages issued after this one (all waves alike)
+      const int ahead = min(kDepth - 2, nst - 1 - s);
+      if (ahead >= 2) wait_vmcnt<2 * (kGroupWLoads + 1)>();
+      else if (ahead == 1) wait_vmcnt<kGroupWLoads + 1>();
+      else wait_vmcnt<0>();
+      // every wave's copies of stage s have landed, and every wave is done
+      // with stage s - 1, whose buffers the next issue refills
+      lds_barrier();
+      if (s + kDepth - 1 < nst) issue(s + kDepth - 1);
+    }
     const uint8_t* wst = wring + (s % kDepth) * kGroupWStage;
     const uint8_t* xst = xring + (s % kDepth) * G::kXStage;
     const int t0 = lo + kSU * s;
