@@ -746,7 +746,19 @@ __global__ void __launch_bounds__(kWideWaves * 64) int4_gemm_strips_wide_kernel(
   const int U = P.units;
   const int lo = p * P.base + min(p, P.rem);
   const int hi = min(lo + P.base + (p < P.rem ? 1 : 0), (P.m / kStripCols) * U);
-  const MagicWords mw = magic_words();
+
+  // Stage s of wave w: units first + W SU s .. + SU - 1 (first = lo + SU w),
+  // so that the workgroup walks W SU consecutive units a round.
+  const int first = lo + kSU * wave;
+  const int nst = first < hi ? (hi - first + W * kSU - 1) / (W * kSU) : 0;
+  uint8_t* wring = smem + wave * G::template wave_bytes<kDepth>();
+  uint8_t* xring = wring + kDepth * G::kWStage;
+  const uint32_t wring_lds = (uint32_t)(uintptr_t)(lds_ptr_t)wring;
+  const uint32_t xring_lds = (uint32_t)(uintptr_t)(lds_ptr_t)xring;
+  float* slots = reinterpret_cast<float*>(smem + W * G::template wave_bytes<kDepth>());
+  uint32_t* lds_status =
+      reinterpret_cast<uint32_t*>(smem + W * G::template wave_bytes<kDepth>() + 2 * W * G::kSlotBytes);
+  float* gate_lds = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(lds_status) + kStatusLdsBytes);
 
   // Weight copies: a wave's stage is SU consecutive units, one contiguous
   // run of 576 SU bytes; slot s = 64 i + lane carries its 16-byte chunk s
@@ -760,6 +772,33 @@ __global__ void __launch_bounds__(kWideWaves * 64) int4_gemm_strips_wide_kernel(
     wfirst[i] = (uint32_t)(16 * (s % 36));
     woff[i] = (uint32_t)(16 * s);
   }
+  // A stage's copies take per-lane offsets fixed for the whole call (a
+  // scalar base moves) unless the stage runs past the range (its weights) or
+  // a unit wraps into the next strip (its X): those stages, uniform
+  // branches, select per lane.
+  auto issue_w = [&](int s) {
+    const int u0 = first + W * kSU * s;
+    const uint8_t* base = P.w + (uint64_t)u0 * kUnitBytes;
+    const uint32_t wst = __builtin_amdgcn_readfirstlane(wring_lds + (s % kDepth) * G::kWStage);
+    if (u0 + kSU <= hi) {
+#pragma unroll
+      for (int i = 0; i < G::kWLoads; ++i)
+        if (i < G::kWLoads - 1 || lane < G::kWTail) lds_dma16(base, woff[i], wst + 1024 * i);
+    } else {
+#pragma unroll
+      for (int i = 0; i < G::kWLoads; ++i) {
+        const uint32_t off = u0 + wunit[i] < hi ? woff[i] : wfirst[i];
+        if (i < G::kWLoads - 1 || lane < G::kWTail) lds_dma16(base, off, wst + 1024 * i);
+      }
+    }
+  };
+  // The first stage's weights go out before the rest of the set-up (its
+  // X, the status word's copy and the read offsets follow; a stage's copies
+  // stay in the order weights, X, and the first ring wait covers all of
+  // them).
+  if (nst > 0) issue_w(0);
+  status_to_lds(P.status, lds_status);
+
   // X copies: copy i, lane l fills position 64 i + l of the stage: row
   // r = position / kRowChunks, chunk c = (position % kRowChunks) ^
   // wide_swz(r), i.e. quarter c % 4 of the stage's unit c / 4 (rows past N
@@ -775,53 +814,8 @@ __global__ void __launch_bounds__(kWideWaves * 64) int4_gemm_strips_wide_kernel(
     xoff[i] = (uint32_t)(2 * (min(r, P.n - 1) * P.k + 8 * (c & 3)));
     xflat[i] = xoff[i] + 64u * (uint32_t)xk[i];  // from the stage's first unit when no unit wraps
   }
-  // LDS reads of unit k of a stage: record q's 8 row scales, the 8 bytes of
-  // column pair j, and quarter q of X row 16 tt + j (past the staged rows:
-  // the last one)
-  const uint32_t rsc = 144 * q, rpay = 144 * q + 16 + 8 * j;
-  uint32_t rx[NT][kSU];
-#pragma unroll
-  for (int tt = 0; tt < NT; ++tt) {
-    const int r = min(16 * tt + j, R - 1);
-#pragma unroll
-    for (int k = 0; k < kSU; ++k) rx[tt][k] = (uint32_t)(16 * (G::kRowChunks * r + ((4 * k + q) ^ wide_swz<SU>(r))));
-  }
-
-  uint8_t* wring = smem + wave * G::template wave_bytes<kDepth>();
-  uint8_t* xring = wring + kDepth * G::kWStage;
-  const uint32_t wring_lds = (uint32_t)(uintptr_t)(lds_ptr_t)wring;
-  const uint32_t xring_lds = (uint32_t)(uintptr_t)(lds_ptr_t)xring;
-  float* slots = reinterpret_cast<float*>(smem + W * G::template wave_bytes<kDepth>());
-  uint32_t* lds_status =
-      reinterpret_cast<uint32_t*>(smem + W * G::template wave_bytes<kDepth>() + 2 * W * G::kSlotBytes);
-  float* gate_lds = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(lds_status) + kStatusLdsBytes);
-  status_to_lds(P.status, lds_status);  // the wave's oldest copy: the first ring wait covers it
-
-  // Stage s of wave w: units first + W SU s .. + SU - 1 (first = lo + SU w),
-  // so that the workgroup walks W SU consecutive units a round.
-  const int first = lo + kSU * wave;
-  const int nst = first < hi ? (hi - first + W * kSU - 1) / (W * kSU) : 0;
-  int ub_issue = first % U;  // strip-relative unit of the next stage's first unit
-
-  // A stage's copies take per-lane offsets fixed for the whole call (a
-  // scalar base moves) unless the stage runs past the range (its weights) or
-  // a unit wraps into the next strip (its X): those stages, uniform
-  // branches, select per lane.
-  auto issue = [&](int s) {
-    const int u0 = first + W * kSU * s;
-    const uint8_t* base = P.w + (uint64_t)u0 * kUnitBytes;
-    const uint32_t wst = __builtin_amdgcn_readfirstlane(wring_lds + (s % kDepth) * G::kWStage);
-    if (u0 + kSU <= hi) {
-#pragma unroll
-      for (int i = 0; i < G::kWLoads; ++i)
-        if (i < G::kWLoads - 1 || lane < G::kWTail) lds_dma16(base, woff[i], wst + 1024 * i);
-    } else {
-#pragma unroll
-      for (int i = 0; i < G::kWLoads; ++i) {
-        const uint32_t off = u0 + wunit[i] < hi ? woff[i] : wfirst[i];
-        if (i < G::kWLoads - 1 || lane < G::kWTail) lds_dma16(base, off, wst + 1024 * i);
-      }
-    }
+  int ub_issue = first % U;  // strip-relative unit of the next X stage's first unit
+  auto issue_x = [&](int s) {  // stages in order
     const uint32_t xst = __builtin_amdgcn_readfirstlane(xring_lds + (s % kDepth) * G::kXStage);
     if (ub_issue + kSU <= U) {
       const uint8_t* xb = reinterpret_cast<const uint8_t*>(P.x) + 64 * ub_issue;
@@ -838,10 +832,28 @@ __global__ void __launch_bounds__(kWideWaves * 64) int4_gemm_strips_wide_kernel(
     ub_issue += W * kSU;
     while (ub_issue >= U) ub_issue -= U;
   };
+  auto issue = [&](int s) {
+    issue_w(s);
+    issue_x(s);
+  };
+  if (nst > 0) issue_x(0);
 #pragma unroll
-  for (int s = 0; s < kDepth - 1; ++s)
+  for (int s = 1; s < kDepth - 1; ++s)
     if (s < nst) issue(s);
   if (nst == 0) wait_vmcnt<0>();  // no ring wait will cover the status copy
+
+  const MagicWords mw = magic_words();
+  // LDS reads of unit k of a stage: record q's 8 row scales, the 8 bytes of
+  // column pair j, and quarter q of X row 16 tt + j (past the staged rows:
+  // the last one)
+  const uint32_t rsc = 144 * q, rpay = 144 * q + 16 + 8 * j;
+  uint32_t rx[NT][kSU];
+#pragma unroll
+  for (int tt = 0; tt < NT; ++tt) {
+    const int r = min(16 * tt + j, R - 1);
+#pragma unroll
+    for (int k = 0; k < kSU; ++k) rx[tt][k] = (uint32_t)(16 * (G::kRowChunks * r + ((4 * k + q) ^ wide_swz<SU>(r))));
+  }
 
   const int strip0 = lo / U;
   const int nparts = hi > lo ? (hi - 1) / U - strip0 + 1 : 0;
