@@ -336,6 +336,97 @@ def measure_projection(torch, timer, lib, config, ns, layout, args, with_floor=T
             "call": call, "row_blob": row_blob}
 
 
+# The reference's native benchmark (antigravity-engine/src/metal_runner.cpp:
+# 120-157): the dense fp16 GEMM at N = 8, K = M = 2048, 0.2638 ms per call on
+# an Apple M1 (30,327.6 tok/s).
+DENSE_CONFIG = ("dense_k2048_m2048", 2048, 2048, [1, 8, 32])
+DENSE_REFERENCE_TOK_S = 30327.6
+
+
+def dense_bytes(N: int, K: int, M: int) -> int:
+    """Algorithmic HBM bytes of one dense call: fp16 W + fp16 X + fp16 Y."""
+    return 2 * K * M + 2 * N * K + 2 * N * M
+
+
+def measure_dense(torch, timer, lib, K, M, ns, args):
+    """The dense fp16 product (``moat_dense_gemm``) per N: graph replay of
+    back-to-back calls over rotated weight copies (> 256 MB), the
+    streaming-read floor of the same weight bytes beside it."""
+    from moat_amd.dense import dense_gemm
+    dev = torch.device("cuda", 0)
+    rng = np.random.default_rng(1010)
+    w0 = torch.from_numpy((0.02 * rng.standard_normal((K, M), dtype=np.float32)).astype(np.float16)).to(dev)
+    copies = max(2, -(-ROTATE_BYTES // (2 * K * M)))
+    ws = [w0] + [w0.clone() for _ in range(copies - 1)]
+    xs = {N: torch.from_numpy(rng.standard_normal((N, K), dtype=np.float32).astype(np.float16)).to(dev) for N in ns}
+    ys = {N: torch.empty((N, M), dtype=torch.float16, device=dev) for N in ns}
+
+    def call(N, i):
+        dense_gemm(xs[N], ws[i % copies], ys[N], splits=args.splits)
+
+    with torch.cuda.stream(timer.cap):
+        for N in ns:  # the capture stream's workspace exists before any capture
+            call(N, 0)
+    torch.cuda.synchronize()
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    wb = 2 * K * M
+
+    def read(i):
+        _lib_check(lib.moat_int4_stream_read(ws[i % copies].data_ptr(), wb, 0, sink.data_ptr(),
+                                             timer.cap.cuda_stream))
+    f_call = timer.per_call_us(read, copies, args.calls)
+    log(f"[bench] dense fp16 K={K} M={M}: {copies} copies of {wb / 1e6:.2f} MB; read floor {f_call:7.2f} us")
+    per_n = {}
+    for N in ns:
+        us = timer.per_call_us(lambda c: call(N, c), copies, args.calls)
+        b = dense_bytes(N, K, M)
+        per_n[str(N)] = {"us_per_call": round(us, 3), "gbs": round(b / us / 1e3, 1),
+                         "roofline_frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4), "tok_s": round(N / us * 1e6, 1),
+                         "algo_bytes": b, "over_read_floor": round(us / f_call, 3)}
+        log(f"[bench]   dense N={N:2d}: {us:8.2f} us/call  {b / us / 1e3:7.0f} GB/s  {us / f_call:.2f}x read floor")
+    del ws
+    return {"workload": f"dense fp16 decode product K={K} M={M} (fp16 weights, fp32 sums, fp16 out)", "K": K,
+            "M": M, "copies": copies, "per_n": per_n,
+            "read_floor": {"bytes": wb, "us_per_call": round(f_call, 3), "gbs": round(wb / f_call / 1e3, 1)}}
+
+
+def run_dense(args) -> int:
+    """The reference's native benchmark shape on the dense fp16 path: value =
+    tokens/s at N = 8 (the shape it times), vs_baseline against its M1
+    figure; the other N and the read floor beside it."""
+    import torch
+    from moat_amd import _lib
+
+    lib = _lib.load()
+    torch.cuda.set_device(0)
+    _, K, M, ns0 = DENSE_CONFIG
+    if args.dense_shape:
+        K, M = (int(v) for v in args.dense_shape.lower().split("x"))
+    ns = [int(v) for v in args.ns.split(",")] if args.ns else ns0
+    timer = Timer(torch)
+    d = measure_dense(torch, timer, lib, K, M, ns, args)
+    dom = "8" if "8" in d["per_n"] else str(ns[0])
+    r = d["per_n"][dom]
+    out = {
+        "metric": "dense fp16 GEMM µs/call and tok/s (the reference's native benchmark shape)",
+        "value": r["tok_s"], "unit": "tok/s", "n_gpus": 1, "steps": args.calls, "warmup": 1,
+        "ms_per_step": round(r["us_per_call"] / 1e3, 6), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": (round(r["tok_s"] / DENSE_REFERENCE_TOK_S, 2)
+                        if dom == "8" and (K, M) == DENSE_CONFIG[1:3] else None),
+        "dtype": "f16", "data": "synthetic",
+        "config": {"workload": d["workload"], "K": K, "M": M, "n": int(dom), "ns": ns,
+                   "weight_copies_rotated": d["copies"]},
+        "per_n": d["per_n"], "read_floor": d["read_floor"],
+        "roofline": {"bound": "hbm", "achieved": r["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": r["roofline_frac"], "traffic": None,
+                     "kernel": f"dense_gemm_kernel N={dom}: {r['algo_bytes']} algorithmic B per call / "
+                               f"{r['us_per_call']} us per call (HIP-graph replay of back-to-back calls)"},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
 def _lib_check(st):
     if st != 0:
         raise RuntimeError(f"libmoat_int4 call failed with status {st}")
@@ -347,12 +438,16 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default=DEFAULT_CONFIG,
-                    choices=sorted(CONFIGS) + ["layer_h2048", "quantize_load"] + sorted(SAMPLE_CONFIGS),
+                    choices=sorted(CONFIGS) + ["layer_h2048", "quantize_load", DENSE_CONFIG[0]]
+                    + sorted(SAMPLE_CONFIGS),
                     help="projection shape (default: K=3072 x M=8192, N = 1..32, with K=8192 x M=28672 "
                          "measured beside it); layer_h2048: one decoder layer's 7 projections at N=16; "
                          "quantize_load: fp16 weights of one layer to INT4 records on the GPU; "
                          "sample_v32000 / sample_v128256: token sampling from V=32000 (K=2048 LM head) or "
-                         "V=128256 (K=4096) logits, alone and after the INT4 LM head")
+                         "V=128256 (K=4096) logits, alone and after the INT4 LM head; dense_k2048_m2048: the "
+                         "dense fp16 product at the reference's native benchmark shape")
+    ap.add_argument("--dense-shape", default=None, metavar="KxM",
+                    help="dense_k2048_m2048: another K x M for the dense fp16 product (fp16 weights)")
     ap.add_argument("--ns", default=None, help="comma-separated N values (default: the config's)")
     ap.add_argument("--algo", type=int, default=0, help="0 auto, 1 dot2, 2 mfma")
     ap.add_argument("--splits", type=int, default=0)
@@ -415,6 +510,8 @@ def main() -> int:
         return run_quantize_load(args)
     if args.config in SAMPLE_CONFIGS:
         return run_sample(args)
+    if args.config == DENSE_CONFIG[0]:
+        return run_dense(args)
 
     import torch
     from moat_amd import _lib
@@ -487,6 +584,14 @@ def main() -> int:
         del d
         torch.cuda.empty_cache()
 
+    dense = None
+    if args.config == DEFAULT_CONFIG and not args.no_side and not args.ns:
+        torch.cuda.empty_cache()
+        dense = measure_dense(torch, timer, lib, DENSE_CONFIG[1], DENSE_CONFIG[2], DENSE_CONFIG[3], args)
+        dense["reference"] = {"n": 8, "tok_s": DENSE_REFERENCE_TOK_S, "hardware": "Apple M1",
+                              "source": "metal_hardware_proof.md:37-42"}
+        torch.cuda.empty_cache()
+
     dom = max(ns, key=lambda n: per_n[n]["us_per_call"])
     roof = {
         "bound": "hbm",
@@ -544,6 +649,7 @@ def main() -> int:
         "read_floor": main_res["read_floor"],
         "largest_projection": side,
         "layer_driver": layer_driver,
+        "dense_fp16": dense,
         "roofline": roof,
         "cpu_baseline": cpu,
     }

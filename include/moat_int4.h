@@ -475,6 +475,34 @@ int32_t moat_sample_tokens(const void* logits, int32_t dtype, int32_t n, int32_t
                            float step, int32_t* tokens, float* logprobs, void* workspace,
                            int64_t workspace_bytes, hipStream_t stream);
 
+/*
+ * Dense fp16 decode product: y[n][m] (fp16) = fp16(f32(x) @ f32(w)), x
+ * [n][k] and w [k][m] row-major fp16, the sums in fp32 and each output
+ * rounded to fp16 once.  Replaces the reference's two dense kernels behind
+ * dispatchGEMM (antigravity-engine/src/transformer_engine.mm:463-500):
+ * batched_gemm_simdgroup (antigravity-engine/src/shaders/
+ * batched_gemm.metal:74-109; half sums, n a multiple of 8), as launched by
+ * metal_runner.cpp:120-143 and antigravity_c_api.cpp:198-216, and the
+ * one-row gemv_kernel (antigravity-engine/src/shaders/
+ * transformer_ops.metal:270-286; fp32 sums, half out).  One entry serves every
+ * n with the GEMV's fp32 sums (the reference's CPU product,
+ * antigravity-engine/tests/test_batched_speed.py:31-42, computes the same);
+ * row r of a call does not depend on the other rows (bit for bit, the
+ * n = 1 call's row).  Preconditions: n >= 1, k >= 8, k % 8 == 0, m >= 8,
+ * m % 8 == 0; x and w 16-byte aligned, y 2-byte aligned and not
+ * overlapping x or w; 0 <= splits <= 1024 (workgroups a 64-column block's
+ * rows are split over; 0 automatic) -- MOAT_ERR_INVALID otherwise.  When
+ * moat_dense_gemm_workspace_size (-1 for an invalid shape) is above 0 the
+ * call needs a 16-byte aligned workspace of that many bytes
+ * (MOAT_ERR_WORKSPACE otherwise), zero-filled before its first use
+ * (moat_int4_workspace_clear) and left with its counter words at zero by
+ * every call; its split sums stay behind, so it is not shared with the
+ * GEMM entry points above.  Calls that overlap on one workspace race.
+ */
+int64_t moat_dense_gemm_workspace_size(int32_t n, int32_t k, int32_t m, int32_t splits);
+int32_t moat_dense_gemm(const uint16_t* x_f16, const uint16_t* w_f16, uint16_t* y_f16, int32_t n, int32_t k,
+                        int32_t m, int32_t splits, void* workspace, int64_t workspace_bytes, hipStream_t stream);
+
 /* ExponentialLUT.lookup (attention.py:60-85): out_f16[i] =
  * lut[size-1-trunc(min(|x[i]| / step, size-1))] for float32 x (NaN -> NaN). */
 int32_t moat_lut_lookup(const float* x, int64_t n, const uint16_t* lut_f16, int32_t lut_size, float step,

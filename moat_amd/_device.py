@@ -131,3 +131,4 @@ class _Workspaces:
 
 workspaces = _Workspaces()  # GEMM calls
 sample_workspaces = _Workspaces()  # sampling calls: their own (they rewrite their counter words)
+dense_workspaces = _Workspaces()  # dense fp16 products: their own (their split sums stay behind)

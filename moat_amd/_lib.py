@@ -53,6 +53,8 @@ SIGNATURES = {
     "moat_int4_records_to_tiles": (_I32, [_P, _I32, _I32, _P, _P]),
     "moat_int4_gemm_tiles": (_I32, [_P, _P, _P, _I32, _I32, _I32, ctypes.POINTER(GemmOptions), _P, _I64, _P]),
     "moat_int4_workspace_clear": (_I32, [_P, _I64, _P]),
+    "moat_dense_gemm_workspace_size": (_I64, [_I32, _I32, _I32, _I32]),
+    "moat_dense_gemm": (_I32, [_P, _P, _P, _I32, _I32, _I32, _I32, _P, _I64, _P]),
     "moat_int4_records_to_strips": (_I32, [_P, _I32, _I32, _P, _P]),
     "moat_int4_strips_to_records": (_I32, [_P, _I32, _I32, _P, _P]),
     "moat_int4_i8_div_to_f16": (_I32, [_P, _I64, ctypes.c_float, _P, _P]),

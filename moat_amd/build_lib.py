@@ -15,7 +15,7 @@ ROOT = os.path.dirname(PKG_DIR)
 CSRC = os.path.join(PKG_DIR, "csrc")
 LIB_NAME = "libmoat_int4.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
-SOURCES = ["abi.hip", "dequant.hip", "gemm.hip", "probe.hip", "quant.hip", "sample.hip", "strips.hip"]
+SOURCES = ["abi.hip", "dense.hip", "dequant.hip", "gemm.hip", "probe.hip", "quant.hip", "sample.hip", "strips.hip"]
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [

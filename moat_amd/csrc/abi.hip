@@ -64,6 +64,11 @@ hipError_t launch_gemm_strip_groups(const uint16_t* x, const uint8_t* w, float* 
 hipError_t launch_gemm_strips_swiglu(const uint16_t* x, const uint8_t* w, uint16_t* h, int n, int k, int m, int wgs,
                                      int per, hipStream_t stream);
 int strip_groups_slot_bytes(int n);
+void dense_plan(int k, int m, int splits_req, int* blocks, int* rounds, int* per, int* splits);
+int64_t dense_slot_bytes(int n, int blocks, int splits);
+int64_t dense_counter_bytes();
+hipError_t launch_dense_gemm(const uint16_t* x, const uint16_t* w, uint16_t* y, int n, int k, int m, int splits_req,
+                             float* slots, uint32_t* counters, hipStream_t stream);
 }  // namespace moat
 
 namespace {
@@ -548,6 +553,30 @@ StripPlan plan_strips(int32_t n, int32_t k, int32_t m, const moat_int4_gemm_opti
 
 int sample_dtype(int32_t dtype) { return dtype == MOAT_DTYPE_F32 ? 0 : dtype == MOAT_DTYPE_F16 ? 1 : 2; }
 
+// Dense fp16 product: rows of X a launch; the workspace holds a fixed area
+// of counter words (one per 64-column block), then the split sums.
+constexpr int32_t kDenseRowsPerLaunch = 32;
+constexpr int32_t kDenseMaxSplits = 1024;
+
+bool dense_shape_ok(int32_t n, int32_t k, int32_t m, int32_t splits) {
+  return n >= 1 && k >= 8 && (k % 8) == 0 && m >= 8 && (m % 8) == 0 && splits >= 0 && splits <= kDenseMaxSplits &&
+         (int64_t)k * m <= ((int64_t)1 << 40) && (int64_t)n * k <= ((int64_t)1 << 40) &&
+         (int64_t)n * m <= ((int64_t)1 << 40);
+}
+
+int64_t dense_workspace_bytes(int32_t n, int32_t k, int32_t m, int32_t splits) {
+  int blocks = 0, rounds = 0, per = 0, sp = 0;
+  moat::dense_plan(k, m, splits, &blocks, &rounds, &per, &sp);
+  if (sp <= 1) return 0;
+  const int rows = n < kDenseRowsPerLaunch ? n : kDenseRowsPerLaunch;
+  return moat::dense_counter_bytes() + moat::dense_slot_bytes(rows, blocks, sp);
+}
+
+bool spans_overlap(const void* a, int64_t a_bytes, const void* b, int64_t b_bytes) {
+  const uintptr_t x = reinterpret_cast<uintptr_t>(a), y = reinterpret_cast<uintptr_t>(b);
+  return x < y + (uintptr_t)b_bytes && y < x + (uintptr_t)a_bytes;
+}
+
 }  // namespace
 
 extern "C" {
@@ -924,6 +953,39 @@ int32_t moat_lut_lookup(const float* x, int64_t n, const uint16_t* lut_f16, int3
   if (!x || !lut_f16 || !out_f16 || !aligned(x, 4) || !aligned(lut_f16, 2) || !aligned(out_f16, 2))
     return MOAT_ERR_INVALID;
   return status_of(moat::launch_lut_lookup(x, n, lut_f16, lut_size, step, out_f16, stream));
+}
+
+int64_t moat_dense_gemm_workspace_size(int32_t n, int32_t k, int32_t m, int32_t splits) {
+  if (!dense_shape_ok(n, k, m, splits)) return -1;
+  return dense_workspace_bytes(n, k, m, splits);
+}
+
+int32_t moat_dense_gemm(const uint16_t* x_f16, const uint16_t* w_f16, uint16_t* y_f16, int32_t n, int32_t k,
+                             int32_t m, int32_t splits, void* workspace, int64_t workspace_bytes,
+                             hipStream_t stream) {
+  if (!dense_shape_ok(n, k, m, splits)) return MOAT_ERR_INVALID;
+  if (!x_f16 || !w_f16 || !y_f16 || !aligned(x_f16, 16) || !aligned(w_f16, 16) || !aligned(y_f16, 2))
+    return MOAT_ERR_INVALID;
+  const int64_t y_bytes = (int64_t)n * m * 2;
+  if (spans_overlap(y_f16, y_bytes, x_f16, (int64_t)n * k * 2) ||
+      spans_overlap(y_f16, y_bytes, w_f16, (int64_t)k * m * 2))
+    return MOAT_ERR_INVALID;  // the output overlaps an input
+  const int64_t need = dense_workspace_bytes(n, k, m, splits);
+  uint32_t* counters = nullptr;
+  float* slots = nullptr;
+  if (need > 0) {
+    if (!workspace || workspace_bytes < need || !aligned(workspace, 16)) return MOAT_ERR_WORKSPACE;
+    counters = static_cast<uint32_t*>(workspace);
+    slots = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + moat::dense_counter_bytes());
+  }
+  // 32 rows of X a launch; the launches share the workspace in stream order
+  for (int32_t r0 = 0; r0 < n; r0 += kDenseRowsPerLaunch) {
+    const int32_t rows = n - r0 < kDenseRowsPerLaunch ? n - r0 : kDenseRowsPerLaunch;
+    const hipError_t e = moat::launch_dense_gemm(x_f16 + (int64_t)r0 * k, w_f16, y_f16 + (int64_t)r0 * m, rows, k, m,
+                                                 splits, slots, counters, stream);
+    if (e != hipSuccess) return MOAT_ERR_HIP;
+  }
+  return MOAT_OK;
 }
 
 }  // extern "C"

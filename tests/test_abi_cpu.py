@@ -378,3 +378,39 @@ def test_gemm_noalloc_validates_before_any_hip_call(lib):
     st = lib.moat_int4_gemm_noalloc(FAKE, FAKE, FAKE, 32, 8192, 32768, None)
     assert st == _lib.MOAT_ERR_TOO_LARGE
     assert b"16 MB" in lib.moat_int4_status_string(st)
+
+
+def test_dense_entry_points_validate(lib):
+    I, W = _lib.MOAT_ERR_INVALID, _lib.MOAT_ERR_WORKSPACE
+    big = ctypes.c_void_p(0x90000000)
+    sz = lib.moat_dense_gemm_workspace_size
+    assert sz(0, 2048, 2048, 0) == -1                       # n < 1
+    assert sz(1, 2044, 2048, 0) == -1                       # k % 8
+    assert sz(1, 2048, 2052, 0) == -1                       # m % 8
+    assert sz(1, 2048, 2048, -1) == -1                      # negative splits
+    assert sz(1, 2048, 2048, 1025) == -1                    # too many splits
+    assert sz(1, 2048, 2048, 1) == 0                        # one split: no workspace
+    assert sz(1, 2048, 2048, 0) > 0                         # 32 blocks split over 8: counters + sums
+    assert sz(32, 2048, 2048, 0) == 16384 + 32 * 8 * 4 * 2 * 1024  # counter area, then the sums
+    assert sz(1, 2048, 64 * 4097, 2) == 0                   # more blocks than counter words: one split
+    assert sz(17, 2048, 2048, 0) == sz(33, 2048, 2048, 0)   # 32 rows a launch
+    # moat_dense_gemm(x, w, y, n, k, m, splits, workspace, workspace_bytes, stream)
+    f = lib.moat_dense_gemm
+    assert f(FAKE, ctypes.c_void_p(0x20000000), big, 0, 2048, 2048, 1, None, 0, None) == I
+    assert f(FAKE, ctypes.c_void_p(0x20000000), big, 1, 2044, 2048, 1, None, 0, None) == I
+    assert f(FAKE, ctypes.c_void_p(0x20000000), big, 1, 2048, 2052, 1, None, 0, None) == I
+    assert f(ctypes.c_void_p(0x10008), ctypes.c_void_p(0x20000000), big, 1, 2048, 2048, 1, None, 0, None) == I
+    assert f(FAKE, ctypes.c_void_p(0x20000008), big, 1, 2048, 2048, 1, None, 0, None) == I   # w 16 B
+    assert f(FAKE, ctypes.c_void_p(0x20000000), ctypes.c_void_p(0x90000001), 1, 2048, 2048, 1, None, 0, None) == I
+    assert f(None, ctypes.c_void_p(0x20000000), big, 1, 2048, 2048, 1, None, 0, None) == I
+    assert f(FAKE, None, big, 1, 2048, 2048, 1, None, 0, None) == I
+    assert f(FAKE, ctypes.c_void_p(0x20000000), None, 1, 2048, 2048, 1, None, 0, None) == I
+    # the output overlaps w
+    assert f(FAKE, ctypes.c_void_p(0x20000000), ctypes.c_void_p(0x20001000), 1, 2048, 2048, 1, None, 0, None) == I
+    # split plans need a workspace of the reported size
+    need = sz(1, 2048, 2048, 0)
+    assert f(FAKE, ctypes.c_void_p(0x20000000), big, 1, 2048, 2048, 0, None, 0, None) == W
+    assert f(FAKE, ctypes.c_void_p(0x20000000), big, 1, 2048, 2048, 0, ctypes.c_void_p(0x70000000), need - 1,
+             None) == W
+    assert f(FAKE, ctypes.c_void_p(0x20000000), big, 1, 2048, 2048, 0, ctypes.c_void_p(0x70000008), need,
+             None) == W
