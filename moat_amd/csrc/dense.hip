@@ -12,26 +12,26 @@
 // X.f32 @ W.f32, cast to W's dtype).
 //
 // Layout and work split (HBM-bound: every weight byte is read once):
-//  * a workgroup (4 waves) owns a 64-column block -- one 128-byte line of
-//    each row -- and a contiguous range of 32-row rounds; the rounds of a
-//    block are split over `splits` workgroups when the blocks alone would
-//    not fill the chip;
-//  * wave w takes every 4th round of the range.  Per round a lane loads four
-//    16-byte pieces of W (rows 4*rg .. 4*rg+3 of the round, columns
-//    8*c8 .. 8*c8+7; eight lanes cover a whole 128-byte line of a row) and,
-//    for each 16-row tile of X, the 16 bytes of its MFMA A operand straight
-//    from X (X is small and stays in L2);
+//  * a workgroup (4 waves) owns a 256-column block -- wave w its 64 columns
+//    64w .. 64w+63, one 128-byte line of each row, so the workgroup reads
+//    512 contiguous bytes of a row at a time -- and a contiguous range of
+//    32-row rounds; a block's rounds are split over `splits` workgroups
+//    when the blocks alone would not fill the chip;
+//  * every wave walks all rounds of the range with 4 rounds of loads in
+//    flight.  Per round a lane loads four 16-byte pieces of W (rows
+//    4*rg .. 4*rg+3 of the round, columns 8*c8 .. 8*c8+7; eight lanes cover
+//    the wave's 128 bytes of a row) and, for each 16-row tile of X, the 16
+//    bytes of its MFMA A operand straight from X (X is small and stays in L2);
 //  * v_mfma_f32_16x16x32_f16 wants each lane's 8 B-operand values along K
 //    (k = 8q .. 8q+7 of column j), while a row-major load gives 8 values
 //    along M: the lane regroups its four rows into k-pairs (two per column)
 //    and writes them to the wave's own LDS tile, column-major (80 bytes a
 //    column: 32 rows of fp16 and 16 bytes of padding), from which each
 //    lane reads its four B operands (16 columns each) as one 16-byte load;
-//  * at the end the 4 waves' sums meet in LDS and wave w adds the column
-//    group w in wave order.  With one split the workgroup writes Y.  With
-//    more, it stores its sums (device-coherent) in its workspace slot and
-//    counts itself in the block's counter; the workgroup that arrives last
-//    adds every split's sums in split order and writes Y, then resets the
+//  * with one split the waves write Y.  With more, each wave stores its sums
+//    (device-coherent) in its workspace slot and the workgroup counts itself
+//    in the block's counter; the workgroup that arrives last loads every
+//    split's sums, adds them in split order and writes Y, then resets the
 //    counter.  No workgroup waits for another; the order of the sums is
 //    fixed, so the bits do not depend on which workgroup arrives last, and
 //    the plan does not depend on N (row r of any N equals the N = 1 call).
@@ -45,17 +45,18 @@ namespace moat {
 namespace {
 
 constexpr int kDenseWaves = 4;
-constexpr int kDenseCols = 64;          // columns of a block
+constexpr int kDenseCols = 64;          // columns of a wave
 constexpr int kDenseRoundRows = 32;     // rows of a round (one MFMA K step)
 constexpr int kDenseColBytes = 80;      // a column of a wave's LDS tile: 32 fp16 rows + 16 padding bytes
 constexpr int kDenseTileBytes = kDenseCols * kDenseColBytes;  // 5120 per wave
 constexpr int kDenseDepth = 4;          // rounds a wave has in flight
+constexpr int kDenseBatch = 4;          // splits whose sums the last workgroup loads at once
 
 struct DenseParams {
   const uint16_t* x;   // [n][k]
   const uint16_t* w;   // [k][m]
   uint16_t* y;         // [n][m]
-  float* slots;        // per (block, split, wave) NT x 64 lanes x 4 floats; null with one split
+  float* slots;        // per (block, split, wave) NT x 4 x 64 lanes x 4 floats; null with one split
   uint32_t* counters;  // one word per block, zero between calls; null with one split
   int n, k, m;
   int rounds;          // ceil(k / 32)
@@ -70,8 +71,11 @@ struct DenseRound {
 };
 
 // Every lane loads from an address inside the matrices (rows and columns
-// clamped) and zeroes what lies outside them, so the loads are not branched
-// around and the ring's wait counts stay exact.
+// clamped), unmasked: the ring carries the loads as they arrive, so no
+// wait falls on the ring's refills.  Past the last column or the last row
+// of X the products land in outputs that are never stored; past row K the
+// round's rows and X's k positions are zeroed when the round is used
+// (dense_mask).
 template <int NT>
 __device__ __forceinline__ void dense_load(const DenseParams& P, int round, int col, bool col_ok, int rg, int q, int i,
                                            DenseRound<NT>& R) {
@@ -80,16 +84,40 @@ __device__ __forceinline__ void dense_load(const DenseParams& P, int round, int 
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int row = k0 + 4 * rg + r;
-    const uint4 v = *reinterpret_cast<const uint4*>(P.w + (int64_t)min(row, P.k - 1) * P.m + colc);
-    const bool ok = col_ok && row < P.k;
-    R.w[r] = make_uint4(ok ? v.x : 0u, ok ? v.y : 0u, ok ? v.z : 0u, ok ? v.w : 0u);
+    R.w[r] = *reinterpret_cast<const uint4*>(P.w + (int64_t)min(row, P.k - 1) * P.m + colc);
   }
   const int xk = k0 + 8 * q;
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     const int xr = 16 * t + i;
-    const half8_t v = *reinterpret_cast<const half8_t*>(P.x + (int64_t)min(xr, P.n - 1) * P.k + min(xk, P.k - 8));
-    R.a[t] = (xr < P.n && xk < P.k) ? v : half8_t{};
+    R.a[t] = *reinterpret_cast<const half8_t*>(P.x + (int64_t)min(xr, P.n - 1) * P.k + min(xk, P.k - 8));
+  }
+}
+
+// Rows k >= K of a round (only the last round of a ragged K has them): W
+// rows and X columns zeroed, so their products vanish.  Straight-line ANDs
+// (no branch, nothing written into a register a load may still fill).
+template <int NT>
+__device__ __forceinline__ void dense_mask(const DenseParams& P, int round, int rg, int q, uint4 (&w)[4],
+                                           half8_t (&a)[NT]) {
+  const int k0 = round * kDenseRoundRows;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const uint32_t keep = k0 + 4 * rg + r < P.k ? 0xFFFFFFFFu : 0u;
+    w[r].x &= keep;
+    w[r].y &= keep;
+    w[r].z &= keep;
+    w[r].w &= keep;
+  }
+  const uint32_t keep_x = k0 + 8 * q < P.k ? 0xFFFFFFFFu : 0u;
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    uint4 v = __builtin_bit_cast(uint4, a[t]);
+    v.x &= keep_x;
+    v.y &= keep_x;
+    v.z &= keep_x;
+    v.w &= keep_x;
+    a[t] = __builtin_bit_cast(half8_t, v);
   }
 }
 
@@ -137,21 +165,26 @@ __device__ __forceinline__ float4_t dense_load_sc1(__amdgpu_buffer_rsrc_t r, int
   return __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kDenseSc1));
 }
 
-template <int NT>
-constexpr int dense_lds_bytes() {
-  return kDenseWaves * kDenseTileBytes > kDenseWaves * NT * 4 * 64 * 16 ? kDenseWaves * kDenseTileBytes
-                                                                         : kDenseWaves * NT * 4 * 64 * 16;
+// WC column groups of 64 a workgroup: 4 (256 columns, wave w the group w,
+// every wave all rounds of the split) or 1 (64 columns, the four waves
+// taking every 4th round and adding their sums in LDS at the end).
+template <int WC>
+constexpr int dense_lds_bytes(int nt) {
+  return WC == 1 && kDenseWaves * nt * 4 * 64 * 16 > kDenseWaves * kDenseTileBytes ? kDenseWaves * nt * 4 * 64 * 16
+                                                                                     : kDenseWaves * kDenseTileBytes;
 }
 
-template <int NT>
+template <int NT, int WC>
 __global__ __launch_bounds__(256) void dense_gemm_kernel(DenseParams P) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[dense_lds_bytes<NT>()];
+  constexpr int G = WC == 4 ? 4 : 1;  // column groups of 16 a wave holds at the end
+  __shared__ __attribute__((aligned(16))) uint8_t lds[dense_lds_bytes<WC>(NT)];
   __shared__ uint32_t last_flag;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int b = blockIdx.x, s = blockIdx.y;
   const int rg = lane >> 3, c8 = lane & 7;  // load role: rows 4rg..4rg+3, columns 8c8..8c8+7
   const int q = lane >> 4, i = lane & 15;   // MFMA role
-  const int col = kDenseCols * b + 8 * c8;
+  const int col0 = WC == 4 ? kDenseCols * (4 * b + wave) : kDenseCols * b;  // the wave's 64 columns
+  const int col = col0 + 8 * c8;
   const bool col_ok = col < P.m;
   const int lo = s * P.per;
   const int hi = min(P.rounds, lo + P.per);
@@ -163,27 +196,36 @@ __global__ __launch_bounds__(256) void dense_gemm_kernel(DenseParams P) {
 #pragma unroll
     for (int g = 0; g < 4; ++g) acc[t][g] = float4_t{0.f, 0.f, 0.f, 0.f};
 
-  // wave w: rounds first, first + 4, ... below hi, kDenseDepth of them in
-  // flight (a ring of registers); a refill past the wave's last round loads
-  // that round again (in the cache), so every pass issues the same loads
-  const int first = lo + wave;
-  const int cnt = first < hi ? (hi - first + kDenseWaves - 1) / kDenseWaves : 0;
+  // the wave's rounds: first, first + step, ... below hi, kDenseDepth of
+  // them in flight (a ring of registers); a refill past the wave's last
+  // round loads that round again (in the cache), so every pass issues the
+  // same loads.  With WC = 4 the workgroup's four waves read 512 contiguous
+  // bytes of each row together.
+  constexpr int step = WC == 4 ? 1 : kDenseWaves;
+  const int first = WC == 4 ? lo : lo + wave;
+  const int cnt = first < hi ? (hi - first + step - 1) / step : 0;
   if (cnt > 0) {
-    const int last = first + kDenseWaves * (cnt - 1);
+    const int last = first + step * (cnt - 1);
     DenseRound<NT> ring[kDenseDepth];
 #pragma unroll
-    for (int j = 0; j < kDenseDepth; ++j)
-      dense_load<NT>(P, min(first + kDenseWaves * j, last), col, col_ok, rg, q, i, ring[j]);
+    for (int j = 0; j < kDenseDepth; ++j) {
+      __builtin_amdgcn_sched_barrier(0);
+      dense_load<NT>(P, min(first + step * j, last), col, col_ok, rg, q, i, ring[j]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
     for (int it = 0; it < cnt; it += kDenseDepth) {
 #pragma unroll
       for (int j = 0; j < kDenseDepth; ++j) {
         const bool live = it + j < cnt;
-        wave_lds_sync();  // the previous round's operand reads are done
-        if (live) dense_stage(tile, rg, c8, ring[j].w);
+        uint4 wv[4];
         half8_t a[NT];
 #pragma unroll
+        for (int r = 0; r < 4; ++r) wv[r] = ring[j].w[r];
+#pragma unroll
         for (int t = 0; t < NT; ++t) a[t] = ring[j].a[t];
-        dense_load<NT>(P, min(first + kDenseWaves * (it + j + kDenseDepth), last), col, col_ok, rg, q, i, ring[j]);
+        dense_mask<NT>(P, first + step * (it + j), rg, q, wv, a);
+        wave_lds_sync();  // the previous round's operand reads are done
+        if (live) dense_stage(tile, rg, c8, wv);
         wave_lds_sync();
         if (live) {
           half8_t bop[4];
@@ -196,36 +238,55 @@ __global__ __launch_bounds__(256) void dense_gemm_kernel(DenseParams P) {
             for (int t = 0; t < NT; ++t)
               acc[t][g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[t], bop[g], acc[t][g], 0, 0, 0);
         }
+        // the entry's registers are free: its next round goes out in place
+        // (the scheduler keeps the ring's load groups in this order, so the
+        // wait for an entry leaves the later entries' loads in flight)
+        __builtin_amdgcn_sched_barrier(0);
+        dense_load<NT>(P, min(first + step * (it + j + kDenseDepth), last), col, col_ok, rg, q, i, ring[j]);
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
   }
 
-  // the 4 waves' sums in LDS, [wave][t][g][lane]; wave w adds column group w
-  __syncthreads();
-  float4_t* red = reinterpret_cast<float4_t*>(lds);
+  // fin[t][gg]: the sums of the wave's output columns ycol0 + 16 gg + i
+  float4_t fin[NT][G];
+  int ycol0;
+  if constexpr (WC == 4) {
 #pragma unroll
-  for (int t = 0; t < NT; ++t)
+    for (int t = 0; t < NT; ++t)
 #pragma unroll
-    for (int g = 0; g < 4; ++g) red[((wave * NT + t) * 4 + g) * 64 + lane] = acc[t][g];
-  __syncthreads();
-  const int g = wave;
-  float4_t sum[NT];
+      for (int g = 0; g < 4; ++g) fin[t][g] = acc[t][g];
+    ycol0 = col0;
+  } else {
+    // the four waves' sums in LDS, [wave][t][g][lane]; wave w adds the
+    // column group w in wave order
+    __syncthreads();
+    float4_t* red = reinterpret_cast<float4_t*>(lds);
 #pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    sum[t] = red[((0 * NT + t) * 4 + g) * 64 + lane];
+    for (int t = 0; t < NT; ++t)
 #pragma unroll
-    for (int v = 1; v < kDenseWaves; ++v) sum[t] += red[((v * NT + t) * 4 + g) * 64 + lane];
+      for (int g = 0; g < 4; ++g) red[((wave * NT + t) * 4 + g) * 64 + lane] = acc[t][g];
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      fin[t][0] = red[((0 * NT + t) * 4 + wave) * 64 + lane];
+#pragma unroll
+      for (int v = 1; v < kDenseWaves; ++v) fin[t][0] += red[((v * NT + t) * 4 + wave) * 64 + lane];
+    }
+    ycol0 = col0 + 16 * wave;
   }
-  // D layout of v_mfma_f32_16x16x32_f16: lane (q, i) holds rows 4q..4q+3, column i
-  const int ycol = kDenseCols * b + 16 * g + i;
 
   if (P.splits > 1) {
-    // the sums out (device-coherent), complete in every wave before the
-    // workgroup counts itself; the last of the block's splits reads them all
+    // the wave's sums out (device-coherent), complete in every wave before
+    // the workgroup counts itself; the last of the block's splits loads all
+    // splits' sums (kDenseBatch splits at a time, every load issued before
+    // the first add) and adds them in split order
     const __amdgpu_buffer_rsrc_t mine =
-        dense_rsrc(P.slots + ((int64_t)(b * P.splits + s) * kDenseWaves + g) * (NT * 256));
+        dense_rsrc(P.slots + ((int64_t)(b * P.splits + s) * kDenseWaves + wave) * (NT * 1024));
 #pragma unroll
-    for (int t = 0; t < NT; ++t) dense_store_sc1(mine, 16 * (64 * t + lane), sum[t]);
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int g = 0; g < G; ++g) dense_store_sc1(mine, 16 * ((G * t + g) * 64 + lane), fin[t][g]);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -234,29 +295,44 @@ __global__ __launch_bounds__(256) void dense_gemm_kernel(DenseParams P) {
     }
     __syncthreads();
     if (last_flag == 0u) return;
-    float4_t tot[NT];
-    for (int s2 = 0; s2 < P.splits; ++s2) {
-      const __amdgpu_buffer_rsrc_t other =
-          dense_rsrc(P.slots + ((int64_t)(b * P.splits + s2) * kDenseWaves + g) * (NT * 256));
+    for (int s0 = 0; s0 < P.splits; s0 += kDenseBatch) {
+      float4_t v[kDenseBatch][NT][G];
 #pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        const float4_t v = s2 == s ? sum[t] : dense_load_sc1(other, 16 * (64 * t + lane));
-        tot[t] = s2 == 0 ? v : tot[t] + v;
+      for (int u = 0; u < kDenseBatch; ++u) {
+        const int s2 = min(s0 + u, P.splits - 1);
+        const __amdgpu_buffer_rsrc_t r =
+            dense_rsrc(P.slots + ((int64_t)(b * P.splits + s2) * kDenseWaves + wave) * (NT * 1024));
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+          for (int g = 0; g < G; ++g) v[u][t][g] = dense_load_sc1(r, 16 * ((G * t + g) * 64 + lane));
+      }
+#pragma unroll
+      for (int u = 0; u < kDenseBatch; ++u) {
+        if (s0 + u < P.splits) {
+#pragma unroll
+          for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int g = 0; g < G; ++g) fin[t][g] = s0 + u == 0 ? v[u][t][g] : fin[t][g] + v[u][t][g];
+        }
       }
     }
-#pragma unroll
-    for (int t = 0; t < NT; ++t) sum[t] = tot[t];
     if (threadIdx.x == 0) __hip_atomic_store(P.counters + b, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 
-  if (ycol < P.m) {
+  // D layout of v_mfma_f32_16x16x32_f16: lane (q, i) holds rows 4q..4q+3, column i
 #pragma unroll
-    for (int t = 0; t < NT; ++t)
+  for (int g = 0; g < G; ++g) {
+    const int ycol = ycol0 + 16 * g + i;
+    if (ycol < P.m) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int row = 16 * t + 4 * q + e;
-        if (row < P.n) P.y[(int64_t)row * P.m + ycol] = __builtin_bit_cast(uint16_t, (_Float16)sum[t][e]);
-      }
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int row = 16 * t + 4 * q + e;
+          if (row < P.n) P.y[(int64_t)row * P.m + ycol] = __builtin_bit_cast(uint16_t, (_Float16)fin[t][g][e]);
+        }
+    }
   }
 }
 
@@ -269,19 +345,31 @@ constexpr int kDenseCounterWords = 4096;
 
 int64_t dense_counter_bytes() { return (int64_t)kDenseCounterWords * 4; }
 
-// Host-side plan, shared with the workspace query: blocks of 64 columns;
-// splits (when not given) so that blocks x splits reaches about 512
-// workgroups with at least 8 rounds (two a wave) per split; one split when
-// the blocks outnumber the counter words (m > 262144: the blocks alone fill
-// the chip).
+// Column groups of 64 a workgroup: 4 (256 columns) from m = 16384 -- long
+// rows, where 512 contiguous bytes per row read keep the stream fast -- and
+// 1 below, where 256-column blocks would be too few to fill the chip.
+int dense_wc(int m) { return m >= 16384 ? 4 : 1; }
+
+// Host-side plan, shared with the workspace query: blocks of 64 x WC
+// columns; splits (when not given) so that blocks x splits reaches about
+// 448 (WC = 4) or 256 (WC = 1) workgroups, with at least 2 rounds a wave
+// per split and at most 16 splits; one split when the blocks outnumber the
+// counter words (m > 1048576: the blocks alone fill the chip).  (Measured:
+// K=2048 x M=5504 11.0 us at 2 splits against 12.3 at 6; K=3072 x M=8192
+// 15.0 at 2 against 17.7 at 4; K=8192 x M=28672 93.3 at 4 against 102.9
+// at 8.)
 void dense_plan(int k, int m, int splits_req, int* blocks, int* rounds, int* per, int* splits) {
-  const int nb = (m + kDenseCols - 1) / kDenseCols;
+  const int wc = dense_wc(m);
+  const int nb = (m + kDenseCols * wc - 1) / (kDenseCols * wc);
   const int nr = (k + kDenseRoundRows - 1) / kDenseRoundRows;
   int sp = splits_req;
   if (sp <= 0) {
-    sp = (512 + nb - 1) / nb;
-    const int most = nr / 8 > 1 ? nr / 8 : 1;
+    const int target = wc == 4 ? 448 : 256;
+    sp = (target + nb - 1) / nb;
+    const int min_rounds = wc == 4 ? 2 : 2 * kDenseWaves;
+    const int most = nr / min_rounds > 1 ? nr / min_rounds : 1;
     if (sp > most) sp = most;
+    if (sp > 16) sp = 16;
   }
   if (nb > kDenseCounterWords) sp = 1;
   if (sp > nr) sp = nr;
@@ -294,7 +382,7 @@ void dense_plan(int k, int m, int splits_req, int* blocks, int* rounds, int* per
 
 int64_t dense_slot_bytes(int n, int blocks, int splits) {
   const int nt = n > 16 ? 2 : 1;
-  return splits > 1 ? (int64_t)blocks * splits * kDenseWaves * nt * 256 * (int64_t)sizeof(float) : 0;
+  return splits > 1 ? (int64_t)blocks * splits * kDenseWaves * nt * 1024 * (int64_t)sizeof(float) : 0;
 }
 
 // n <= 32 rows a launch; counters and slots as the plan needs (null with one split).
@@ -312,10 +400,14 @@ hipError_t launch_dense_gemm(const uint16_t* x, const uint16_t* w, uint16_t* y, 
   int blocks = 0;
   dense_plan(k, m, splits_req, &blocks, &P.rounds, &P.per, &P.splits);
   const dim3 grid(blocks, P.splits), block(256);
-  if (n > 16)
-    hipLaunchKernelGGL(dense_gemm_kernel<2>, grid, block, 0, stream, P);
-  else
-    hipLaunchKernelGGL(dense_gemm_kernel<1>, grid, block, 0, stream, P);
+  const bool wide = dense_wc(m) == 4;
+  if (n > 16) {
+    if (wide) hipLaunchKernelGGL((dense_gemm_kernel<2, 4>), grid, block, 0, stream, P);
+    else hipLaunchKernelGGL((dense_gemm_kernel<2, 1>), grid, block, 0, stream, P);
+  } else {
+    if (wide) hipLaunchKernelGGL((dense_gemm_kernel<1, 4>), grid, block, 0, stream, P);
+    else hipLaunchKernelGGL((dense_gemm_kernel<1, 1>), grid, block, 0, stream, P);
+  }
   return hipGetLastError();
 }
 

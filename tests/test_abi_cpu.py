@@ -391,8 +391,8 @@ def test_dense_entry_points_validate(lib):
     assert sz(1, 2048, 2048, 1025) == -1                    # too many splits
     assert sz(1, 2048, 2048, 1) == 0                        # one split: no workspace
     assert sz(1, 2048, 2048, 0) > 0                         # 32 blocks split over 8: counters + sums
-    assert sz(32, 2048, 2048, 0) == 16384 + 32 * 8 * 4 * 2 * 1024  # counter area, then the sums
-    assert sz(1, 2048, 64 * 4097, 2) == 0                   # more blocks than counter words: one split
+    assert sz(32, 2048, 2048, 0) == 16384 + 32 * 8 * 4 * 2 * 4096  # counter area, then the sums
+    assert sz(1, 2048, 256 * 4097, 2) == 0                  # more blocks than counter words: one split
     assert sz(17, 2048, 2048, 0) == sz(33, 2048, 2048, 0)   # 32 rows a launch
     # moat_dense_gemm(x, w, y, n, k, m, splits, workspace, workspace_bytes, stream)
     f = lib.moat_dense_gemm
