@@ -407,6 +407,32 @@ def run_dense(args) -> int:
     d = measure_dense(torch, timer, lib, K, M, ns, args)
     dom = "8" if "8" in d["per_n"] else str(ns[0])
     r = d["per_n"][dom]
+    cpu = None
+    if not args.no_cpu_baseline:
+        # the reference's CPU product (test_batched_speed.py:31-42): fp16(f32(X) @ f32(W)), the
+        # oracle's dense_gemm_ref, on the host's BLAS threads; median of 3-10 calls per N
+        sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+        from oracle import dense_oracle as DO
+        info = _thread_info()
+        rng = np.random.default_rng(1011)
+        w_h = (0.02 * rng.standard_normal((K, M))).astype(np.float16)
+        per = {}
+        for N in ns:
+            x_h = rng.standard_normal((N, K)).astype(np.float16)
+            DO.dense_gemm_ref(x_h, w_h)
+            times, t_start = [], time.perf_counter()
+            while len(times) < 3 or (time.perf_counter() - t_start < args.cpu_budget / len(ns) and len(times) < 10):
+                t0 = time.perf_counter()
+                DO.dense_gemm_ref(x_h, w_h)
+                times.append(time.perf_counter() - t0)
+            med = float(np.median(times))
+            per[str(N)] = {"ms_per_call": round(med * 1e3, 3), "tok_s": round(N / med, 1), "reps": len(times)}
+        c = per.get(dom, per[str(ns[0])])
+        cpu = {"value": c["tok_s"], "unit": "tok/s", "cores": info.get("blas_threads"), "kind": "port",
+               "sample": f"fp16(f32(X) @ f32(W)) (oracle dense_gemm_ref, the reference's CPU product) at "
+                         f"N = {dom}, K = {K}, M = {M}; every N timed, median of 3-10 calls",
+               "per_n": per, "threads": info}
+        log(f"[bench] CPU baseline: {c['tok_s']:.1f} tok/s at N={dom} ({info.get('blas_threads')} BLAS threads)")
     out = {
         "metric": "dense fp16 GEMM µs/call and tok/s (the reference's native benchmark shape)",
         "value": r["tok_s"], "unit": "tok/s", "n_gpus": 1, "steps": args.calls, "warmup": 1,
@@ -421,7 +447,7 @@ def run_dense(args) -> int:
                      "frac": r["roofline_frac"], "traffic": None,
                      "kernel": f"dense_gemm_kernel N={dom}: {r['algo_bytes']} algorithmic B per call / "
                                f"{r['us_per_call']} us per call (HIP-graph replay of back-to-back calls)"},
-        "cpu_baseline": None,
+        "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
     return 0
