@@ -351,25 +351,26 @@ int64_t dense_counter_bytes() { return (int64_t)kDenseCounterWords * 4; }
 int dense_wc(int m) { return m >= 16384 ? 4 : 1; }
 
 // Host-side plan, shared with the workspace query: blocks of 64 x WC
-// columns; splits (when not given) so that blocks x splits reaches about
-// 448 (WC = 4) or 256 (WC = 1) workgroups, with at least 2 rounds a wave
-// per split and at most 16 splits; one split when the blocks outnumber the
-// counter words (m > 1048576: the blocks alone fill the chip).  (Measured:
-// K=2048 x M=5504 11.0 us at 2 splits against 12.3 at 6; K=3072 x M=8192
-// 15.0 at 2 against 17.7 at 4; K=8192 x M=28672 93.3 at 4 against 102.9
-// at 8.)
+// columns; splits (when not given) the largest power of two that keeps
+// blocks x splits within 256 (WC = 1) or 448 (WC = 4) workgroups, with at
+// least 2 rounds a wave per split and at most 16 splits -- powers of two
+// keep a split's rounds a multiple of the ring depth; one split when the
+// blocks outnumber the counter words (m > 1048576: the blocks alone fill
+// the chip).  (Measured, us at N = 1: K=2048 x M=5504 11.0 at 2 splits,
+// 11.5 at 4, 12.3 at 6; K=3072 x M=8192 15.0 at 2, 17.7 at 4; K=8192 x
+// M=28672 93.8 at 4, 99.2 at 2, 107.2 at 3, 109.8 at 5, 102.9 at 8;
+// K=4096 x M=16384 31.1 at 4, 53.6 at 2, 38.6 at 3; K=2048 x M=32000 30.8
+// at 2, 31.2 at 4, 34.9 at 3.)
 void dense_plan(int k, int m, int splits_req, int* blocks, int* rounds, int* per, int* splits) {
   const int wc = dense_wc(m);
   const int nb = (m + kDenseCols * wc - 1) / (kDenseCols * wc);
   const int nr = (k + kDenseRoundRows - 1) / kDenseRoundRows;
   int sp = splits_req;
   if (sp <= 0) {
-    const int target = wc == 4 ? 448 : 256;
-    sp = (target + nb - 1) / nb;
+    const int most_wgs = wc == 4 ? 448 : 256;
     const int min_rounds = wc == 4 ? 2 : 2 * kDenseWaves;
-    const int most = nr / min_rounds > 1 ? nr / min_rounds : 1;
-    if (sp > most) sp = most;
-    if (sp > 16) sp = 16;
+    sp = 1;
+    while (sp < 16 && (int64_t)nb * sp * 2 <= most_wgs && nr / (sp * 2) >= min_rounds) sp *= 2;
   }
   if (nb > kDenseCounterWords) sp = 1;
   if (sp > nr) sp = nr;
