@@ -213,39 +213,47 @@ __global__ __launch_bounds__(256) void dense_gemm_kernel(DenseParams P) {
       dense_load<NT>(P, min(first + step * j, last), col, col_ok, rg, q, i, ring[j]);
     }
     __builtin_amdgcn_sched_barrier(0);
-    for (int it = 0; it < cnt; it += kDenseDepth) {
+    // one round of the ring: entry j holds round first + step * (it + j)
+    auto use = [&](int it, int j, bool live) {
+      uint4 wv[4];
+      half8_t a[NT];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) wv[r] = ring[j].w[r];
+#pragma unroll
+      for (int t = 0; t < NT; ++t) a[t] = ring[j].a[t];
+      dense_mask<NT>(P, first + step * (it + j), rg, q, wv, a);
+      wave_lds_sync();  // the previous round's operand reads are done
+      if (live) dense_stage(tile, rg, c8, wv);
+      wave_lds_sync();
+      if (live) {
+        half8_t bop[4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          bop[g] = *reinterpret_cast<const half8_t*>(tile + (16 * g + i) * kDenseColBytes + 16 * q);
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+          for (int t = 0; t < NT; ++t)
+            acc[t][g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[t], bop[g], acc[t][g], 0, 0, 0);
+      }
+    };
+    // full passes: after each use the entry's registers are free and its
+    // next round goes out in place (the scheduler keeps the ring's load
+    // groups in this order, so the wait for an entry leaves the later
+    // entries' loads in flight); the last pass issues no loads, so no
+    // load is left for the end of the kernel to wait on
+    int it = 0;
+    for (; it + kDenseDepth < cnt; it += kDenseDepth) {
 #pragma unroll
       for (int j = 0; j < kDenseDepth; ++j) {
-        const bool live = it + j < cnt;
-        uint4 wv[4];
-        half8_t a[NT];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) wv[r] = ring[j].w[r];
-#pragma unroll
-        for (int t = 0; t < NT; ++t) a[t] = ring[j].a[t];
-        dense_mask<NT>(P, first + step * (it + j), rg, q, wv, a);
-        wave_lds_sync();  // the previous round's operand reads are done
-        if (live) dense_stage(tile, rg, c8, wv);
-        wave_lds_sync();
-        if (live) {
-          half8_t bop[4];
-#pragma unroll
-          for (int g = 0; g < 4; ++g)
-            bop[g] = *reinterpret_cast<const half8_t*>(tile + (16 * g + i) * kDenseColBytes + 16 * q);
-#pragma unroll
-          for (int g = 0; g < 4; ++g)
-#pragma unroll
-            for (int t = 0; t < NT; ++t)
-              acc[t][g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[t], bop[g], acc[t][g], 0, 0, 0);
-        }
-        // the entry's registers are free: its next round goes out in place
-        // (the scheduler keeps the ring's load groups in this order, so the
-        // wait for an entry leaves the later entries' loads in flight)
+        use(it, j, true);
         __builtin_amdgcn_sched_barrier(0);
         dense_load<NT>(P, min(first + step * (it + j + kDenseDepth), last), col, col_ok, rg, q, i, ring[j]);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
+#pragma unroll
+    for (int j = 0; j < kDenseDepth; ++j) use(it, j, it + j < cnt);
   }
 
   // fin[t][gg]: the sums of the wave's output columns ycol0 + 16 gg + i
