@@ -55,6 +55,8 @@ def dense_gemm(x, w, out=None, *, splits: int = 0):
     if out is not None and D.is_tensor(out):
         if out.dtype != torch.float16 or tuple(out.shape) != (N, M) or not out.is_contiguous():
             raise ValueError(f"out must be a contiguous float16 tensor of shape {(N, M)}")
+        if out.device != xs.device:
+            raise ValueError(f"out must be on {xs.device} (got {out.device})")
         y = out
     else:
         y = torch.empty((N, M), dtype=torch.float16, device=xs.device)

@@ -126,6 +126,12 @@ def test_python_checks():
         dense_gemm(x, torch.ones((8, 16), dtype=torch.float16, device="cuda"))    # K mismatch
     with pytest.raises(ValueError):
         dense_gemm(x.float(), torch.ones((16, 16), dtype=torch.float16, device="cuda"))  # dtype
+    with pytest.raises(ValueError):
+        dense_gemm(x, torch.ones((16, 16), dtype=torch.float16, device="cuda"),
+                   torch.empty((2, 16), dtype=torch.float16))                      # out on the host
+    with pytest.raises(ValueError):
+        dense_gemm(x, torch.ones((16, 16), dtype=torch.float16, device="cuda"),
+                   torch.empty((2, 8), dtype=torch.float16, device="cuda"))        # out shape
     out = torch.empty((2, 16), dtype=torch.float16, device="cuda")
     y = dense_gemm(x, torch.full((16, 16), 0.25, dtype=torch.float16, device="cuda"), out)
     assert y is out and torch.all(out == 4.0).item()
