@@ -165,25 +165,28 @@ __device__ __forceinline__ float4_t dense_load_sc1(__amdgpu_buffer_rsrc_t r, int
   return __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kDenseSc1));
 }
 
-// WC column groups of 64 a workgroup: 4 (256 columns, wave w the group w,
-// every wave all rounds of the split) or 1 (64 columns, the four waves
-// taking every 4th round and adding their sums in LDS at the end).
+// WC column groups of 64 a workgroup (1, 2 or 4): wave w reads group
+// w % WC and every (4 / WC)-th round of the split from round w / WC; the
+// 4 / WC waves of a group add their sums in LDS at the end, each finishing
+// WC of the group's four 16-column tiles.
 template <int WC>
 constexpr int dense_lds_bytes(int nt) {
-  return WC == 1 && kDenseWaves * nt * 4 * 64 * 16 > kDenseWaves * kDenseTileBytes ? kDenseWaves * nt * 4 * 64 * 16
-                                                                                     : kDenseWaves * kDenseTileBytes;
+  return WC < 4 && kDenseWaves * nt * 4 * 64 * 16 > kDenseWaves * kDenseTileBytes ? kDenseWaves * nt * 4 * 64 * 16
+                                                                                    : kDenseWaves * kDenseTileBytes;
 }
 
 template <int NT, int WC>
 __global__ __launch_bounds__(256) void dense_gemm_kernel(DenseParams P) {
-  constexpr int G = WC == 4 ? 4 : 1;  // column groups of 16 a wave holds at the end
+  constexpr int G = WC;                 // 16-column tiles a wave finishes
+  constexpr int R = kDenseWaves / WC;   // waves sharing a column group
   __shared__ __attribute__((aligned(16))) uint8_t lds[dense_lds_bytes<WC>(NT)];
   __shared__ uint32_t last_flag;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int b = blockIdx.x, s = blockIdx.y;
   const int rg = lane >> 3, c8 = lane & 7;  // load role: rows 4rg..4rg+3, columns 8c8..8c8+7
   const int q = lane >> 4, i = lane & 15;   // MFMA role
-  const int col0 = WC == 4 ? kDenseCols * (4 * b + wave) : kDenseCols * b;  // the wave's 64 columns
+  const int cg = wave % WC, ro = wave / WC;                 // column group, first round
+  const int col0 = kDenseCols * (WC * b + cg);              // the wave's 64 columns
   const int col = col0 + 8 * c8;
   const bool col_ok = col < P.m;
   const int lo = s * P.per;
@@ -201,8 +204,8 @@ __global__ __launch_bounds__(256) void dense_gemm_kernel(DenseParams P) {
   // round loads that round again (in the cache), so every pass issues the
   // same loads.  With WC = 4 the workgroup's four waves read 512 contiguous
   // bytes of each row together.
-  constexpr int step = WC == 4 ? 1 : kDenseWaves;
-  const int first = WC == 4 ? lo : lo + wave;
+  constexpr int step = R;
+  const int first = lo + ro;
   const int cnt = first < hi ? (hi - first + step - 1) / step : 0;
   if (cnt > 0) {
     const int last = first + step * (cnt - 1);
@@ -256,18 +259,19 @@ __global__ __launch_bounds__(256) void dense_gemm_kernel(DenseParams P) {
     for (int j = 0; j < kDenseDepth; ++j) use(it, j, it + j < cnt);
   }
 
-  // fin[t][gg]: the sums of the wave's output columns ycol0 + 16 gg + i
+  // fin[t][g]: the sums of the wave's output columns ycol0 + 16 g + i
   float4_t fin[NT][G];
   int ycol0;
-  if constexpr (WC == 4) {
+  if constexpr (R == 1) {
 #pragma unroll
     for (int t = 0; t < NT; ++t)
 #pragma unroll
       for (int g = 0; g < 4; ++g) fin[t][g] = acc[t][g];
     ycol0 = col0;
   } else {
-    // the four waves' sums in LDS, [wave][t][g][lane]; wave w adds the
-    // column group w in wave order
+    // the sums in LDS, [wave][t][tile][lane]; wave (cg, ro) adds tiles
+    // ro * G .. ro * G + G - 1 of group cg over the group's R waves, in
+    // round order
     __syncthreads();
     float4_t* red = reinterpret_cast<float4_t*>(lds);
 #pragma unroll
@@ -276,12 +280,15 @@ __global__ __launch_bounds__(256) void dense_gemm_kernel(DenseParams P) {
       for (int g = 0; g < 4; ++g) red[((wave * NT + t) * 4 + g) * 64 + lane] = acc[t][g];
     __syncthreads();
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      fin[t][0] = red[((0 * NT + t) * 4 + wave) * 64 + lane];
+    for (int t = 0; t < NT; ++t)
 #pragma unroll
-      for (int v = 1; v < kDenseWaves; ++v) fin[t][0] += red[((v * NT + t) * 4 + wave) * 64 + lane];
-    }
-    ycol0 = col0 + 16 * wave;
+      for (int g = 0; g < G; ++g) {
+        const int tile16 = ro * G + g;
+        fin[t][g] = red[((cg * NT + t) * 4 + tile16) * 64 + lane];
+#pragma unroll
+        for (int v = 1; v < R; ++v) fin[t][g] += red[(((v * WC + cg) * NT + t) * 4 + tile16) * 64 + lane];
+      }
+    ycol0 = col0 + 16 * G * ro;
   }
 
   if (P.splits > 1) {
@@ -356,6 +363,7 @@ int64_t dense_counter_bytes() { return (int64_t)kDenseCounterWords * 4; }
 // Column groups of 64 a workgroup: 4 (256 columns) from m = 16384 -- long
 // rows, where 512 contiguous bytes per row read keep the stream fast -- and
 // 1 below, where 256-column blocks would be too few to fill the chip.
+// (128-column blocks measured 0-9 % slower than 64 at m = 5504..14336.)
 int dense_wc(int m) { return m >= 16384 ? 4 : 1; }
 
 // Host-side plan, shared with the workspace query: blocks of 64 x WC
@@ -376,7 +384,7 @@ void dense_plan(int k, int m, int splits_req, int* blocks, int* rounds, int* per
   int sp = splits_req;
   if (sp <= 0) {
     const int most_wgs = wc == 4 ? 448 : 256;
-    const int min_rounds = wc == 4 ? 2 : 2 * kDenseWaves;
+    const int min_rounds = 2 * (kDenseWaves / wc);
     sp = 1;
     while (sp < 16 && (int64_t)nb * sp * 2 <= most_wgs && nr / (sp * 2) >= min_rounds) sp *= 2;
   }
@@ -409,12 +417,12 @@ hipError_t launch_dense_gemm(const uint16_t* x, const uint16_t* w, uint16_t* y, 
   int blocks = 0;
   dense_plan(k, m, splits_req, &blocks, &P.rounds, &P.per, &P.splits);
   const dim3 grid(blocks, P.splits), block(256);
-  const bool wide = dense_wc(m) == 4;
+  const int wc = dense_wc(m);
   if (n > 16) {
-    if (wide) hipLaunchKernelGGL((dense_gemm_kernel<2, 4>), grid, block, 0, stream, P);
+    if (wc == 4) hipLaunchKernelGGL((dense_gemm_kernel<2, 4>), grid, block, 0, stream, P);
     else hipLaunchKernelGGL((dense_gemm_kernel<2, 1>), grid, block, 0, stream, P);
   } else {
-    if (wide) hipLaunchKernelGGL((dense_gemm_kernel<1, 4>), grid, block, 0, stream, P);
+    if (wc == 4) hipLaunchKernelGGL((dense_gemm_kernel<1, 4>), grid, block, 0, stream, P);
     else hipLaunchKernelGGL((dense_gemm_kernel<1, 1>), grid, block, 0, stream, P);
   }
   return hipGetLastError();
