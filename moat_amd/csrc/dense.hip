@@ -12,23 +12,27 @@
 // X.f32 @ W.f32, cast to W's dtype).
 //
 // Layout and work split (HBM-bound: every weight byte is read once):
-//  * a workgroup (4 waves) owns a 256-column block -- wave w its 64 columns
-//    64w .. 64w+63, one 128-byte line of each row, so the workgroup reads
-//    512 contiguous bytes of a row at a time -- and a contiguous range of
-//    32-row rounds; a block's rounds are split over `splits` workgroups
-//    when the blocks alone would not fill the chip;
-//  * every wave walks all rounds of the range with 4 rounds of loads in
-//    flight.  Per round a lane loads four 16-byte pieces of W (rows
-//    4*rg .. 4*rg+3 of the round, columns 8*c8 .. 8*c8+7; eight lanes cover
-//    the wave's 128 bytes of a row) and, for each 16-row tile of X, the 16
-//    bytes of its MFMA A operand straight from X (X is small and stays in L2);
+//  * a workgroup (4 waves) owns a block of 64 x WC columns and a contiguous
+//    range of 32-row rounds.  WC = 4 for long rows (M >= 16384): wave w
+//    takes the 64 columns 64w .. 64w+63, one 128-byte line of each row, over
+//    every round, so the workgroup reads 512 contiguous bytes of a row at a
+//    time.  WC = 1 below that, where 256-column blocks would be too few:
+//    the four waves share 64 columns and take every 4th round.  A block's
+//    rounds are split over `splits` workgroups when the blocks alone would
+//    not fill the chip;
+//  * each wave keeps 4 rounds of loads in flight.  Per round a lane loads
+//    four 16-byte pieces of W (rows 4*rg .. 4*rg+3 of the round, columns
+//    8*c8 .. 8*c8+7; eight lanes cover the wave's 128 bytes of a row) and,
+//    for each 16-row tile of X, the 16 bytes of its MFMA A operand straight
+//    from X (X is small and stays in L2);
 //  * v_mfma_f32_16x16x32_f16 wants each lane's 8 B-operand values along K
 //    (k = 8q .. 8q+7 of column j), while a row-major load gives 8 values
 //    along M: the lane regroups its four rows into k-pairs (two per column)
 //    and writes them to the wave's own LDS tile, column-major (80 bytes a
 //    column: 32 rows of fp16 and 16 bytes of padding), from which each
 //    lane reads its four B operands (16 columns each) as one 16-byte load;
-//  * with one split the waves write Y.  With more, each wave stores its sums
+//  * waves that share columns add their sums in LDS (in round order);
+//    with one split the waves write Y.  With more, each wave stores its sums
 //    (device-coherent) in its workspace slot and the workgroup counts itself
 //    in the block's counter; the workgroup that arrives last loads every
 //    split's sums, adds them in split order and writes Y, then resets the
