@@ -58,6 +58,7 @@ WORKLOAD_NAMES = {
     "k5632_m2048": "int4 superblock down projection of a hidden-2048 layer (K=5632, M=2048)",
 }
 ROTATE_BYTES = 300 * 1024 * 1024
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 matrix peak (information: the path is HBM-bound)
 DEFAULT_CONFIG = "k3072_m8192"
 # measured beside the default workload: the largest single-GPU projection
 SIDE_CONFIG = ("k8192_m28672", [1, 8, 32])
@@ -321,9 +322,11 @@ def measure_projection(torch, timer, lib, config, ns, layout, args, with_floor=T
     for N in ns:
         us = timer.per_call_us(lambda c: call(N, c), copies, args.calls)
         b = algo_bytes(N, K, M)
+        tflops = 2.0 * N * K * M / us / 1e6
         per_n[N] = {"us_per_call": round(us, 3), "gbs": round(b / us / 1e3, 1),
                     "roofline_frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4), "tok_s": round(N / us * 1e6, 1),
-                    "algo_bytes": b}
+                    "algo_bytes": b, "tflops": round(tflops, 2),
+                    "mfma_frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 5)}
         if floor:
             per_n[N]["over_read_floor"] = round(us / floor["us_per_call"], 3)
         log(f"[bench]   N={N:2d}: {us:8.2f} us/call  {b / us / 1e3:7.0f} GB/s  "
